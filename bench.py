@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Throughput of the futon encoder forward on one MI355X.
+
+Workload: bge-small-shaped BERT encoder (12 layers, hidden 384, 12 heads,
+FFN 1536, erf-GELU, absolute positions, CLS pooling + L2), fp32 seeded
+synthetic weights written as a futon pack and loaded through LoadModel;
+batch 256 of [CLS] + Zipf(1.1) ids + [SEP], lengths uniform in 16..128,
+packed without padding.  One step = one forward over the whole batch with
+ids already resident in HBM (fh_encode_device on torch's current stream).
+
+Prints ONE JSON line: embeddings/s, plus the dominant kernel's roofline
+(per-launch algorithmic FLOPs over its HIP-event-timed average duration)
+and a CPU baseline (the oracle on the host cores, a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+PEAK_I8_TOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+GEMM_CLASSES = ("gemm_qkv", "gemm_out", "gemm_ffn1", "gemm_fc2")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="bge-small")
+    ap.add_argument("--pack-root", default=os.path.join(tempfile.gettempdir(), "futon_bench_packs"))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def flops_per_embedding(cfg: dict, L: int) -> float:
+    """Algorithmic FLOPs of one unpadded forward (valid tokens only), the
+    reference's algorithm including the CLS last-layer shortcut."""
+    H, I, N = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_layers"]
+    c = 6 if cfg["activation"] == "swiglu" else 4
+    full = (8 * H * H + c * H * I) * L + 4 * H * L * L
+    if cfg["pooling"] == "cls":
+        last = 6 * H * H * L + 4 * H * L + 2 * H * H + c * H * I
+        return (N - 1) * full + last
+    return N * full
+
+
+def cpu_baseline(w, cfg, tensors, ids, offsets, target_s: float):
+    import oracle
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    om = oracle.Model(cfg, tensors, q8=w.q8)
+    nseq = offsets.size - 1
+    # probe on `threads` sequences, then size the sample to ≈ target_s
+    n0 = min(nseq, threads)
+    t0 = time.perf_counter()
+    om.encode_batch(ids[:offsets[n0]], offsets[:n0 + 1], w.out_dim, threads)
+    dt = time.perf_counter() - t0
+    n = int(min(nseq, max(n0, n0 * target_s / max(dt, 1e-3))))
+    t0 = time.perf_counter()
+    om.encode_batch(ids[:offsets[n]], offsets[:n + 1], w.out_dim, threads)
+    dt = time.perf_counter() - t0
+    om.close()
+    return {"value": round(n / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "sample": f"first {n} of the {nseq} sequences of the same batch, oracle/oracle.c "
+                      f"(restated reference forward, AVX2-order GEMM) on {threads} OpenMP threads, "
+                      f"one sequence per thread as the reference's batchPlan at large batch; {dt:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from futon_amd import native, synth
+
+    w = synth.workload(args.workload)
+    cfg = w.config
+    pack = synth.ensure_workload_pack(w, args.pack_root)
+    model = native.LoadModel(pack, q8=w.q8)
+    ids, offsets = synth.make_batch(w.ids_seed, w.batch, w.len_lo, w.len_hi)
+    lens = np.diff(offsets)
+    nseq, T, max_len = int(lens.size), int(offsets[-1]), int(lens.max())
+    od = w.out_dim or cfg["hidden_size"]
+
+    dev = torch.device("cuda:0")
+    d_ids = torch.from_numpy(ids).to(dev)
+    d_off = torch.from_numpy(offsets).to(dev)
+    d_out = torch.empty((nseq, od), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step():
+        model.EncodeDevice(d_ids.data_ptr(), d_off.data_ptr(), nseq, T, max_len, w.out_dim, d_out.data_ptr(), sp,
+                           offsets)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    value = nseq * args.steps / elapsed
+
+    # Per-kernel-class HIP-event timing over the same number of steps.
+    model.profile_reset()
+    model.profile_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = model.profile_read()
+    model.profile_enable(False)
+    dom = max(prof, key=lambda k: prof[k]["ms"])
+    pd = prof[dom]
+    per_launch_ms = pd["ms"] / max(pd["launches"], 1)
+    if pd["flops"] > 0:
+        peak = PEAK_I8_TOPS if w.q8 and dom.startswith("gemm") else PEAK_F16_TFLOPS
+        achieved = pd["flops"] / pd["launches"] / (per_launch_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": None,
+                "per_launch_flops": pd["flops"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3)}
+    else:
+        achieved = pd["bytes"] / pd["launches"] / (per_launch_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "per_launch_bytes": pd["bytes"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3)}
+    gemm_ms = sum(prof[k]["ms"] for k in GEMM_CLASSES)
+    gemm_fl = sum(prof[k]["flops"] for k in GEMM_CLASSES)
+    gemm_tf = gemm_fl / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+    total_fl = float(sum(flops_per_embedding(cfg, int(L)) for L in lens))
+    kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 4), "launches_per_step": v["launches"] // args.steps,
+                   "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1) if v["ms"] and v["flops"] else None,
+                   "gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1) if v["ms"] and v["bytes"] else None}
+               for k, v in prof.items() if v["launches"]}
+
+    # End-to-end with host buffers (PCIe-inclusive), reported beside value.
+    batch_list = None
+    t0 = time.perf_counter()
+    reps = max(3, args.steps // 5)
+    for _ in range(reps):
+        model.EncodePacked(ids, offsets, w.out_dim)
+    host_rate = nseq * reps / (time.perf_counter() - t0)
+    del batch_list
+
+    result = {
+        "metric": "embeddings/sec at 1 MI355X (bge-small, B=256, L<=128); % MFMA peak",
+        "value": round(value, 1), "unit": "embeddings/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8" if w.q8 else "f16",
+        "data": "synthetic (seeded random-init weights, Zipf ids)",
+        "config": {"workload": f"{w.name}: {cfg['num_layers']}L H{cfg['hidden_size']} A{cfg['num_heads']} "
+                               f"I{cfg['intermediate_size']} {cfg['activation']} {cfg['pooling']}-pool, "
+                               f"B={nseq}, L {w.len_lo}..{w.len_hi} (T={T} tokens, packed)",
+                   "global_batch": nseq, "seq_len": max_len, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "gemm_mfma": {"tflops": round(gemm_tf, 1), "frac": round(gemm_tf / (PEAK_I8_TOPS if w.q8 else PEAK_F16_TFLOPS), 4)},
+        "model_tflops": round(total_fl * value / nseq / 1e12, 1),
+        "model_mfma_frac": round(total_fl * value / nseq / 1e12 / (PEAK_I8_TOPS if w.q8 else PEAK_F16_TFLOPS), 4),
+        "host_buffers_value": round(host_rate, 1),
+        "kernels": kernels,
+    }
+    if not args.no_cpu:
+        tensors = synth.make_tensors(cfg, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+        result["cpu_baseline"] = cpu_baseline(w, cfg, tensors, ids, offsets, args.cpu_seconds)
+    model.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

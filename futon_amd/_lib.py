@@ -1,0 +1,110 @@
+"""ctypes binding of futon_amd/libfuton_hip.so (include/futon_hip.h and
+include/futon_hip_ops.h).  The library is the only compute path: if it is not
+built, importing the model API raises; there is no CPU fallback."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfuton_hip.so")
+
+FH_OK = 0
+FH_EINVAL = -22
+FH_ENOMEM = -12
+FH_EHIP = -5
+FH_ECANCELED = -125
+FH_ETOOLONG = -36
+FH_ENODEV = -19
+
+FH_POS_ABSOLUTE, FH_POS_ROPE = 0, 1
+FH_ACT_GELU, FH_ACT_SWIGLU = 0, 1
+FH_POOL_MEAN, FH_POOL_CLS = 0, 1
+FH_DTYPE_F32, FH_DTYPE_F16 = 0, 1
+FH_OP_F16, FH_OP_I8 = 0, 1
+FH_OP_ACT_NONE, FH_OP_ACT_GELU, FH_OP_ACT_SWIGLU = 0, 1, 2
+
+# Every symbol the public headers declare (checked by the CPU test suite).
+EXPORTED = (
+    "fh_model_create", "fh_model_destroy", "fh_encode", "fh_encode_device", "fh_profile_enable",
+    "fh_profile_reset", "fh_profile_read", "fh_debug_cancel_after", "fh_checkpoints_per_call",
+    "fh_strerror", "fh_last_error", "fh_model_device_bytes",
+    "fh_op_gemm", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
+    "fh_op_pool",
+)
+
+
+class FhConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", ctypes.c_int32), ("num_layers", ctypes.c_int32), ("num_heads", ctypes.c_int32),
+        ("intermediate_size", ctypes.c_int32), ("vocab_size", ctypes.c_int32),
+        ("type_vocab_size", ctypes.c_int32), ("max_seq_len", ctypes.c_int32),
+        ("max_trained_positions", ctypes.c_int32), ("layer_norm_eps", ctypes.c_double),
+        ("position_encoding", ctypes.c_int32), ("rope_theta", ctypes.c_double),
+        ("activation", ctypes.c_int32), ("pooling", ctypes.c_int32), ("normalize", ctypes.c_int32),
+        ("matryoshka", ctypes.c_int32), ("matryoshka_layernorm", ctypes.c_int32), ("q8", ctypes.c_int32),
+    ]
+
+
+class FhTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int32), ("rank", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 4), ("data", ctypes.c_void_p)]
+
+
+class FutonError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """Loads the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run futon_amd/build.py (no CPU fallback exists)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32 = ctypes.c_void_p, ctypes.c_int32
+    L.fh_model_create.restype = ctypes.c_int
+    L.fh_model_create.argtypes = [ctypes.POINTER(FhConfig), ctypes.POINTER(FhTensor), i32, i32, ctypes.POINTER(vp)]
+    L.fh_model_destroy.restype = None
+    L.fh_model_destroy.argtypes = [vp]
+    L.fh_encode.restype = ctypes.c_int
+    L.fh_encode.argtypes = [vp, vp, vp, i32, i32, vp, vp]
+    L.fh_encode_device.restype = ctypes.c_int
+    L.fh_encode_device.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]
+    L.fh_profile_enable.argtypes = [vp, i32]
+    L.fh_profile_reset.argtypes = [vp]
+    L.fh_profile_read.argtypes = [vp, vp, vp, vp, vp, vp, i32]
+    L.fh_debug_cancel_after.argtypes = [vp, i32]
+    L.fh_checkpoints_per_call.argtypes = [vp]
+    L.fh_strerror.restype = ctypes.c_char_p
+    L.fh_strerror.argtypes = [ctypes.c_int]
+    L.fh_last_error.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+    L.fh_model_device_bytes.restype = ctypes.c_int64
+    L.fh_model_device_bytes.argtypes = [vp]
+    L.fh_op_gemm.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    L.fh_op_attention.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, i32, i32, vp]
+    L.fh_op_layer_norm.argtypes = [vp, i32, i32, vp, vp, ctypes.c_float, vp, vp, vp]
+    L.fh_op_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
+    L.fh_op_embed_ln.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, ctypes.c_float, i32, vp, vp, vp]
+    L.fh_op_pool.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(2048)
+    load().fh_last_error(buf, 2048)
+    return buf.value.decode(errors="replace")
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != FH_OK:
+        detail = last_error()
+        name = load().fh_strerror(rc).decode()
+        raise FutonError(rc, f"{what}: {name} ({rc}): {detail}" if what else f"{name} ({rc}): {detail}")

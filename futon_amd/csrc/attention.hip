@@ -1,0 +1,217 @@
+// Varlen multi-head self-attention over packed sequences on gfx950 MFMA.
+//
+// Replaces the reference's per-head attendHead + softmaxScaled
+// (native/model.go:646-739): scores = q·kᵀ, softmax(scores/√d) per query
+// row, out = P·v, written to the head's columns of the concatenated output.
+// The reference runs each sequence unpadded; here sequences are packed
+// back to back (offsets[]) and every key outside the query's own sequence
+// is excluded, which is the same function.  RoPE (rotateHalf,
+// model.go:705-712) is applied to q and k as they are staged.
+//
+// Block = (query block of 16·WAVES rows, head, sequence).  K and V of a
+// 64-key block are staged once per block in LDS (V transposed).  Each wave
+// computes Sᵀ = K·Qᵀ with v_mfma_f32_16x16x32_f16 so that a lane owns four
+// scores of ONE query (lane%16); the online-softmax statistics of a query
+// therefore live in the lanes that also own its output column, and P feeds
+// the Oᵀ = Vᵀ·Pᵀ MFMA straight from registers (the key order inside the
+// contraction is permuted identically on both operands).
+#include "fh_common.h"
+
+namespace {
+
+constexpr int KBLK = 64;  // keys per staged block
+
+template <int D, int WAVES, bool OUT_F32, bool ROPE>
+__global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
+    constexpr int QROWS = 16 * WAVES;
+    constexpr int KS = D + 8;      // K / Q LDS row stride (halves)
+    constexpr int VS = KBLK + 8;   // Vᵀ LDS row stride (halves)
+    __shared__ __attribute__((aligned(16))) f16 Qs[QROWS * KS];
+    __shared__ __attribute__((aligned(16))) f16 Ks[KBLK * KS];
+    __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
+
+    const int seq = blockIdx.z, head = blockIdx.y;
+    const int start = a.offsets[seq];
+    const int L = a.offsets[seq + 1] - start;
+    const int nq = min(L, a.q_limit);
+    const int q0 = blockIdx.x * QROWS;
+    if (q0 >= nq) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int d = a.d, H = a.H, ld = 3 * H;
+    const int half = d >> 1;
+    const int chunks = d >> 3;  // 16-byte chunks per row (d % 8 == 0)
+    const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+    // ── stage Q (rows clamped into the sequence; padding dims zero) ──
+    for (int c = tid; c < QROWS * (D / 8); c += WAVES * 64) {
+        const int r = c / (D / 8), ch = c % (D / 8);
+        const int q = min(q0 + r, L - 1);
+        f16x8 v = z8;
+        if (ch < chunks) v = *(const f16x8 *)(a.qkv + (size_t)(start + q) * ld + head * d + ch * 8);
+        *(f16x8 *)&Qs[r * KS + ch * 8] = v;
+    }
+    __syncthreads();
+    if (ROPE) {
+        for (int c = tid; c < QROWS * half; c += WAVES * 64) {
+            const int r = c / half, i = c % half;
+            const int pos = min(q0 + r, L - 1);
+            const float cs = a.rope_cos[pos * half + i], sn = a.rope_sin[pos * half + i];
+            const float x1 = (float)Qs[r * KS + i], x2 = (float)Qs[r * KS + i + half];
+            Qs[r * KS + i] = (f16)(x1 * cs - x2 * sn);
+            Qs[r * KS + i + half] = (f16)(x2 * cs + x1 * sn);
+        }
+        __syncthreads();
+    }
+    // B operand of Sᵀ = K·Qᵀ: lane holds dims [dk·32 + (lane/16)·8, +8) of query lane%16.
+    f16x8 qf[D / 32];
+#pragma unroll
+    for (int dk = 0; dk < D / 32; ++dk)
+        qf[dk] = *(const f16x8 *)&Qs[(wave * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
+
+    f32x4 o[D / 16];
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const float sl2 = a.scale_log2e;
+
+    for (int kb0 = 0; kb0 < L; kb0 += KBLK) {
+        __syncthreads();  // previous block's K/V fully consumed
+        for (int c = tid; c < KBLK * (D / 8); c += WAVES * 64) {
+            const int r = c / (D / 8), ch = c % (D / 8);
+            const int key = min(kb0 + r, L - 1);
+            const f16 *row = a.qkv + (size_t)(start + key) * ld + head * d + ch * 8;
+            f16x8 kv = z8, vv = z8;
+            if (ch < chunks) {
+                kv = *(const f16x8 *)(row + H);
+                vv = *(const f16x8 *)(row + 2 * H);
+            }
+            *(f16x8 *)&Ks[r * KS + ch * 8] = kv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Vt[(ch * 8 + j) * VS + r] = vv[j];
+        }
+        __syncthreads();
+        if (ROPE) {
+            for (int c = tid; c < KBLK * half; c += WAVES * 64) {
+                const int r = c / half, i = c % half;
+                const int pos = min(kb0 + r, L - 1);
+                const float cs = a.rope_cos[pos * half + i], sn = a.rope_sin[pos * half + i];
+                const float x1 = (float)Ks[r * KS + i], x2 = (float)Ks[r * KS + i + half];
+                Ks[r * KS + i] = (f16)(x1 * cs - x2 * sn);
+                Ks[r * KS + i + half] = (f16)(x2 * cs + x1 * sn);
+            }
+            __syncthreads();
+        }
+
+        // Sᵀ tiles: s[kt][i] = score(key kb0 + kt·16 + (lane/16)·4 + i, query lane%16).
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dk = 0; dk < D / 32; ++dk) {
+                const f16x8 kf =
+                    *(const f16x8 *)&Ks[(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dk], s[kt], 0, 0, 0);
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kb0 + kt * 16 + (lane >> 4) * 4 + i;
+                if (key >= L) s[kt][i] = -INFINITY;
+                mx = fmaxf(mx, s[kt][i]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx * sl2);  // log2-scaled running max
+        const float corr = exp2f(m_run - m_new);
+        float psum = 0.f;
+        f16x8 pf[2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = exp2f(s[kt][i] * sl2 - m_new);
+                psum += p;
+                pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * corr + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) o[t] *= corr;
+
+        // Oᵀ += Vᵀ·Pᵀ over two 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) {
+                const f16 *vrow = &Vt[(t * 16 + (lane & 15)) * VS + c * 32 + (lane >> 4) * 4];
+                const f16x4 lo = *(const f16x4 *)vrow;
+                const f16x4 hi = *(const f16x4 *)(vrow + 16);
+                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4].
+    const int q = q0 + wave * 16 + (lane & 15);
+    if (q >= nq) return;
+    const float inv = 1.0f / l_run;
+    const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+        const int dim = t * 16 + (lane >> 4) * 4;
+        if (dim >= d) continue;
+        const f32x4 v = o[t] * inv;
+        if (OUT_F32) {
+            *(f32x4 *)((float *)a.out + orow * a.ldo + head * d + dim) = v;
+        } else {
+            const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+            *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * d + dim) = h;
+        }
+    }
+}
+
+template <int D, int WAVES>
+hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope,
+                    hipStream_t s) {
+    constexpr int QROWS = 16 * WAVES;
+    const int qmax = min(max_len, a.q_limit);
+    dim3 grid((qmax + QROWS - 1) / QROWS, a.H / a.d, nseq);
+    dim3 block(WAVES * 64);
+    if (out_f32) {
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, true, false>), grid, block, 0, s, a);
+    } else {
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, false, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, false, false>), grid, block, 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope,
+                    hipStream_t s) {
+    // One wave per (sequence, head) when only the CLS row is queried.
+    if (a.q_limit <= 16) return launch_d<D, 1>(a, nseq, max_len, out_f32, rope, s);
+    return launch_d<D, 4>(a, nseq, max_len, out_f32, rope, s);
+}
+
+}  // namespace
+
+namespace fh {
+hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s) {
+    if (nseq <= 0 || max_len <= 0) return hipSuccess;
+    const bool rope = a.rope_cos != nullptr;
+    if (a.d <= 32) return launch_w<32>(a, nseq, max_len, out_f32, rope, s);
+    if (a.d <= 64) return launch_w<64>(a, nseq, max_len, out_f32, rope, s);
+    if (a.d <= 128) return launch_w<128>(a, nseq, max_len, out_f32, rope, s);
+    return hipErrorInvalidValue;
+}
+}  // namespace fh

@@ -1,0 +1,882 @@
+// Host orchestration behind include/futon_hip.h: weight upload, workspace,
+// per-batch kernel schedule, cancellation checkpoints, profiling.
+//
+// The schedule is the reference forward (native/model.go:346-457,
+// :550-635) over a packed batch:
+//   embed+LN → per layer { QKV GEMM → attention → out GEMM(+bias+residual)
+//   → LN → FFN GEMM(+bias, GELU | SwiGLU) → fc2 GEMM(+bias+residual) → LN }
+//   → pool → Matryoshka → L2.
+// With CLS pooling the last layer computes only each sequence's row 0 after
+// the attention (model.go:403-410): the CLS rows are gathered into a compact
+// [nseq, H] buffer and the out/FFN GEMMs run with M = nseq.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/futon_hip.h"
+#include "fh_common.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                       \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess) return fail(FH_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// Exact binary16 → binary32 (native/safetensors.go:266-289).
+float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31, exp = (h >> 10) & 0x1f, mant = h & 0x3ff, bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            uint32_t e = 127 - 15 + 1;
+            while (!(mant & 0x400)) {
+                mant <<= 1;
+                e--;
+            }
+            bits = sign | e << 23 | (mant & 0x3ff) << 13;
+        }
+    } else if (exp == 0x1f) {
+        bits = sign | 0xffu << 23 | mant << 13;
+    } else {
+        bits = sign | (exp + 127 - 15) << 23 | mant << 13;
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// binary32 → binary16, round to nearest even (native/safetensors.go:226-262).
+uint16_t f32_to_f16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    uint16_t sign = (uint16_t)(b >> 16) & 0x8000;
+    int32_t exp32 = (int32_t)(b >> 23 & 0xff), exp = exp32 - 127 + 15;
+    uint32_t mant = b & 0x7fffff;
+    if (exp32 == 0xff) return mant ? (sign | 0x7e00) : (sign | 0x7c00);
+    if (exp >= 0x1f) return sign | 0x7c00;
+    if (exp <= 0) {
+        if (exp < -10) return sign;
+        mant |= 0x800000;
+        uint32_t shift = (uint32_t)(14 - exp), half = mant >> shift, rem = mant & ((1u << shift) - 1),
+                 hw = 1u << (shift - 1);
+        if (rem > hw || (rem == hw && (half & 1))) half++;
+        return sign | (uint16_t)half;
+    }
+    uint16_t half = (uint16_t)((uint32_t)exp << 10 | (mant >> 13));
+    uint32_t rem = mant & 0x1fff;
+    if (rem > 0x1000 || (rem == 0x1000 && (half & 1))) half++;
+    return sign | half;
+}
+
+// Per-row absmax int8 quantization (native/quant.go:42-70); float64 rounding
+// half away from zero like math.Round.
+float quantize_row_q8(int8_t *dst, const float *src, int n) {
+    float amax = 0.f;
+    for (int i = 0; i < n; i++) amax = std::max(amax, std::fabs(src[i]));
+    if (amax == 0.f) {
+        memset(dst, 0, (size_t)n);
+        return 0.f;
+    }
+    const float scale = amax / 127.0f;
+    const double inv = 127.0 / (double)amax;
+    for (int i = 0; i < n; i++) {
+        double q = std::round((double)src[i] * inv);
+        q = std::min(127.0, std::max(-127.0, q));
+        dst[i] = (int8_t)q;
+    }
+    return scale;
+}
+
+struct DevMat {
+    void *w = nullptr;       // f16 [n,k] or i8 [n,k]
+    float *scale = nullptr;  // i8: [n]
+    int n = 0, k = 0;
+};
+
+struct DevLayer {
+    DevMat qkv, out, ffn1, fc2;  // ffn1 = fc1, or fc1|gate interleaved in 16-row blocks (SwiGLU)
+    float *qkv_b = nullptr, *out_b = nullptr, *ffn1_b = nullptr, *fc2_b = nullptr;
+    float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+};
+
+enum KClass {
+    K_EMBED, K_GEMM_QKV, K_ATTN, K_GEMM_OUT, K_LN, K_GEMM_FFN1, K_GEMM_FC2, K_QUANT, K_GATHER, K_POOL,
+    K_NCLASS
+};
+const char *kClassNames[K_NCLASS] = {"embed_ln",  "gemm_qkv", "attention", "gemm_out",
+                                     "layer_norm", "gemm_ffn1", "gemm_fc2", "quantize_rows",
+                                     "gather_cls", "pool_l2"};
+
+struct ProfPending {
+    int cls;
+    hipEvent_t a, b;
+    double flops, bytes;
+};
+
+}  // namespace
+
+struct fh_model {
+    fh_config cfg{};
+    int device = 0, hd = 0, eff_max = 0;
+    hipStream_t stream = nullptr;
+    float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    std::vector<DevLayer> layers;
+    std::vector<void *> allocs;
+    int64_t weight_bytes = 0;
+
+    // Workspace, grown on demand (capacity in tokens / sequences).
+    int cap_tokens = 0, cap_seqs = 0;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    float *x32 = nullptr, *y32 = nullptr, *xc32 = nullptr, *out = nullptr;
+    f16 *x16 = nullptr, *qkv = nullptr, *xc16 = nullptr;
+    void *attn = nullptr, *attnc = nullptr, *hbuf = nullptr;
+    int8_t *xq = nullptr;
+    float *xs = nullptr;
+    int32_t *ids = nullptr, *offsets = nullptr;
+    // Pinned host staging for fh_encode.
+    void *pin = nullptr;
+    size_t pin_bytes = 0;
+
+    std::mutex mu;
+    int cancel_after = -1;
+    bool prof = false;
+    std::vector<ProfPending> pending;
+    std::vector<hipEvent_t> event_pool;
+    double prof_ms[K_NCLASS] = {}, prof_flops[K_NCLASS] = {}, prof_bytes[K_NCLASS] = {};
+    int64_t prof_launches[K_NCLASS] = {};
+};
+
+namespace {
+
+template <class T>
+int dev_alloc(fh_model *m, T **p, size_t bytes) {
+    void *q = nullptr;
+    hipError_t e = hipMalloc(&q, std::max<size_t>(bytes, 256));
+    if (e != hipSuccess) return fail(FH_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    m->allocs.push_back(q);
+    m->weight_bytes += (int64_t)bytes;
+    *p = (T *)q;
+    return FH_OK;
+}
+
+template <class T>
+int upload(fh_model *m, T **p, const void *host, size_t bytes) {
+    int rc = dev_alloc(m, p, bytes);
+    if (rc) return rc;
+    HIPCHK(hipMemcpy(*p, host, bytes, hipMemcpyHostToDevice));
+    return FH_OK;
+}
+
+struct TensorView {
+    const fh_tensor *t = nullptr;
+    int64_t numel() const {
+        int64_t n = 1;
+        for (int i = 0; i < t->rank; i++) n *= t->shape[i];
+        return n;
+    }
+    // Element i as float32 (f16 converted exactly).
+    void to_f32(std::vector<float> &dst) const {
+        const int64_t n = numel();
+        dst.resize((size_t)n);
+        if (t->dtype == FH_DTYPE_F32) {
+            memcpy(dst.data(), t->data, (size_t)n * 4);
+        } else {
+            const uint16_t *s = (const uint16_t *)t->data;
+            for (int64_t i = 0; i < n; i++) dst[(size_t)i] = f16_to_f32(s[i]);
+        }
+    }
+};
+
+struct Loader {
+    fh_model *m;
+    const fh_tensor *ts;
+    int n;
+    std::vector<bool> used;
+    std::string model_id = "pack";
+
+    int find(const std::string &name) const {
+        for (int i = 0; i < n; i++)
+            if (ts[i].name && name == ts[i].name) return i;
+        return -1;
+    }
+    // needT (native/model.go:143-158): presence, rank and shape.
+    int need(const std::string &name, std::initializer_list<int64_t> shape, TensorView &tv,
+             bool optional = false, bool *present = nullptr) {
+        const int i = find(name);
+        if (present) *present = i >= 0;
+        if (i < 0) {
+            if (optional) return FH_OK;
+            return fail(FH_EINVAL, "pack %s: missing tensor \"%s\"", model_id.c_str(), name.c_str());
+        }
+        used[(size_t)i] = true;
+        const fh_tensor &t = ts[i];
+        if (t.rank != (int)shape.size())
+            return fail(FH_EINVAL, "pack %s: tensor \"%s\" rank %d, want %d", model_id.c_str(), name.c_str(),
+                        t.rank, (int)shape.size());
+        int j = 0;
+        for (int64_t d : shape) {
+            if (t.shape[j] != d)
+                return fail(FH_EINVAL, "pack %s: tensor \"%s\" dim %d is %lld, want %lld", model_id.c_str(),
+                            name.c_str(), j, (long long)t.shape[j], (long long)d);
+            j++;
+        }
+        if (t.dtype != FH_DTYPE_F32 && t.dtype != FH_DTYPE_F16)
+            return fail(FH_EINVAL, "pack %s: tensor \"%s\" has unsupported dtype %d", model_id.c_str(),
+                        name.c_str(), t.dtype);
+        if (!t.data) return fail(FH_EINVAL, "pack %s: tensor \"%s\" has no data", model_id.c_str(), name.c_str());
+        tv.t = &t;
+        return FH_OK;
+    }
+    int vec_f32(const std::string &name, int64_t len, float **dst, bool optional = false) {
+        TensorView tv;
+        bool present = true;
+        int rc = need(name, {len}, tv, optional, &present);
+        if (rc || !present) return rc;
+        std::vector<float> h;
+        tv.to_f32(h);
+        return upload(m, dst, h.data(), h.size() * 4);
+    }
+    int mat_f32(const std::string &name, int64_t r, int64_t c, float **dst) {
+        TensorView tv;
+        int rc = need(name, {r, c}, tv);
+        if (rc) return rc;
+        std::vector<float> h;
+        tv.to_f32(h);
+        return upload(m, dst, h.data(), h.size() * 4);
+    }
+    int mat_host(const std::string &name, int64_t r, int64_t c, std::vector<float> &h) {
+        TensorView tv;
+        int rc = need(name, {r, c}, tv);
+        if (rc) return rc;
+        tv.to_f32(h);
+        return FH_OK;
+    }
+};
+
+// Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales.
+int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8) {
+    d.n = n;
+    d.k = k;
+    if (q8) {
+        std::vector<int8_t> codes((size_t)n * k);
+        std::vector<float> sc((size_t)n);
+        for (int j = 0; j < n; j++) sc[(size_t)j] = quantize_row_q8(&codes[(size_t)j * k], &w[(size_t)j * k], k);
+        int rc = upload(m, (int8_t **)&d.w, codes.data(), codes.size());
+        if (rc) return rc;
+        return upload(m, &d.scale, sc.data(), sc.size() * 4);
+    }
+    std::vector<uint16_t> h(w.size());
+    for (size_t i = 0; i < w.size(); i++) h[i] = f32_to_f16(w[i]);
+    return upload(m, (uint16_t **)&d.w, h.data(), h.size() * 2);
+}
+
+// SwiGLU packing: packed row r → fc1 row 16·(r/32) + r%32 when r%32 < 16,
+// else gate row 16·(r/32) + r%32 − 16.
+void interleave16(const std::vector<float> &up, const std::vector<float> &gate, int I, int k,
+                  std::vector<float> &dst) {
+    dst.resize((size_t)2 * I * k);
+    for (int r = 0; r < 2 * I; r++) {
+        const int blk = r / 32, w = r % 32;
+        const std::vector<float> &src = w < 16 ? up : gate;
+        const int sr = 16 * blk + (w % 16);
+        memcpy(&dst[(size_t)r * k], &src[(size_t)sr * k], (size_t)k * 4);
+    }
+}
+
+int eff_max_len(const fh_config &c) {
+    return (c.max_trained_positions > 0 && c.max_trained_positions < c.max_seq_len) ? c.max_trained_positions
+                                                                                     : c.max_seq_len;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int ensure_workspace(fh_model *m, int tokens, int seqs) {
+    if (tokens <= m->cap_tokens && seqs <= m->cap_seqs) return FH_OK;
+    const int T = std::max(tokens, m->cap_tokens), S = std::max(seqs, m->cap_seqs);
+    const size_t H = (size_t)m->cfg.hidden_size, I = (size_t)m->cfg.intermediate_size;
+    const bool q8 = m->cfg.q8 != 0;
+    const size_t hsz = q8 ? 4 : 2;  // FFN hidden / attention output element size
+    size_t off = 0;
+    std::vector<std::pair<void **, size_t>> plan = {
+        {(void **)&m->x32, (size_t)T * H * 4},        {(void **)&m->x16, (size_t)T * H * 2},
+        {(void **)&m->qkv, (size_t)T * 3 * H * 2},    {(void **)&m->attn, (size_t)T * H * hsz},
+        {(void **)&m->y32, (size_t)T * H * 4},        {(void **)&m->hbuf, (size_t)T * I * hsz},
+        {(void **)&m->xc32, (size_t)S * H * 4},       {(void **)&m->xc16, (size_t)S * H * 2},
+        {(void **)&m->attnc, (size_t)S * H * hsz},    {(void **)&m->out, (size_t)S * H * 4},
+        {(void **)&m->ids, (size_t)T * 4},            {(void **)&m->offsets, (size_t)(S + 1) * 4},
+    };
+    if (q8) {
+        plan.push_back({(void **)&m->xq, (size_t)T * std::max(H, I)});
+        plan.push_back({(void **)&m->xs, (size_t)T * 4});
+    }
+    std::vector<size_t> offs;
+    for (auto &p : plan) {
+        offs.push_back(off);
+        off += align256(p.second);
+    }
+    if (m->ws) {
+        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(hipFree(m->ws));
+        m->ws = nullptr;
+    }
+    hipError_t e = hipMalloc(&m->ws, off);
+    if (e != hipSuccess) return fail(FH_ENOMEM, "workspace hipMalloc(%zu): %s", off, hipGetErrorString(e));
+    m->ws_bytes = off;
+    for (size_t i = 0; i < plan.size(); i++) *plan[i].first = (char *)m->ws + offs[i];
+    m->cap_tokens = T;
+    m->cap_seqs = S;
+    return FH_OK;
+}
+
+// ── profiling ──
+struct Scope {
+    fh_model *m;
+    int cls;
+    double flops, bytes;
+    hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t s;
+    Scope(fh_model *m_, int c, double f, double by, hipStream_t st) : m(m_), cls(c), flops(f), bytes(by), s(st) {
+        if (!m->prof) return;
+        a = take();
+        b = take();
+        hipEventRecord(a, s);
+    }
+    hipEvent_t take() {
+        if (m->event_pool.empty()) {
+            hipEvent_t e;
+            hipEventCreate(&e);
+            return e;
+        }
+        hipEvent_t e = m->event_pool.back();
+        m->event_pool.pop_back();
+        return e;
+    }
+    ~Scope() {
+        if (!m->prof) return;
+        hipEventRecord(b, s);
+        m->pending.push_back({cls, a, b, flops, bytes});
+    }
+};
+
+void drain_profile(fh_model *m) {
+    for (auto &p : m->pending) {
+        float ms = 0.f;
+        hipEventSynchronize(p.b);
+        hipEventElapsedTime(&ms, p.a, p.b);
+        m->prof_ms[p.cls] += ms;
+        m->prof_flops[p.cls] += p.flops;
+        m->prof_bytes[p.cls] += p.bytes;
+        m->prof_launches[p.cls] += 1;
+        m->event_pool.push_back(p.a);
+        m->event_pool.push_back(p.b);
+    }
+    m->pending.clear();
+}
+
+struct BatchInfo {
+    const int32_t *d_ids, *d_offsets;
+    int nseq, T, max_len, out_dim;
+    float *d_out;
+    double sum_l2 = 0.0;  // Σ L_i², for attention FLOP accounting
+    const volatile int32_t *cancel = nullptr;
+    bool host_checks = false;  // cancellation checkpoints active
+};
+
+#define LCHK(expr)                                                                         \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess) return fail(FH_EHIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+int checkpoint(fh_model *m, const BatchInfo &b, int &cp, hipStream_t s) {
+    const int idx = cp++;
+    if (!b.host_checks) return FH_OK;
+    const bool hit = (b.cancel && *b.cancel != 0) || (m->cancel_after >= 0 && idx == m->cancel_after);
+    if (hit) {
+        hipStreamSynchronize(s);
+        return fail(FH_ECANCELED, "native: context canceled at checkpoint %d", idx);
+    }
+    return FH_OK;
+}
+
+int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const float *a_scale, int M,
+         const float *bias, const float *resid, int ldr, void *C, int ldc, int act, bool out_f32,
+         hipStream_t s) {
+    GemmArgs g{};
+    g.A = A;
+    g.B = w.w;
+    g.bias = bias;
+    g.resid = resid;
+    g.a_scale = a_scale;
+    g.b_scale = w.scale;
+    g.C = C;
+    g.M = M;
+    g.N = w.n;
+    g.K = w.k;
+    g.lda = lda;
+    g.ldb = w.k;
+    g.ldc = ldc;
+    g.ldr = ldr;
+    const bool i8 = w.scale != nullptr;
+    const double flops = 2.0 * M * (double)w.n * w.k;
+    const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
+    const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
+                         (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : 0.0);
+    Scope sc(m, cls, flops, bytes, s);
+    LCHK(i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
+    return FH_OK;
+}
+
+int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s) {
+    Scope sc(m, K_QUANT, 0.0, (double)M * K * 5, s);
+    LCHK(fh::quantize_rows(x, M, K, ldx, m->xq, m->xs, s));
+    return FH_OK;
+}
+
+int layer_norm(fh_model *m, const float *y, int M, const float *gw, const float *gb, float *x32, f16 *x16,
+               hipStream_t s) {
+    const int H = m->cfg.hidden_size;
+    Scope sc(m, K_LN, 0.0, (double)M * H * (4 + 4 + 2), s);
+    LCHK(fh::layer_norm(y, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
+    return FH_OK;
+}
+
+int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
+    const fh_config &c = m->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
+    const bool q8 = c.q8 != 0, cls = c.pooling == FH_POOL_CLS, swiglu = c.activation == FH_ACT_SWIGLU;
+    const float eps = (float)c.layer_norm_eps;
+    int cp = 0, rc;
+
+    {
+        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + 6) + T * 4.0, s);
+        LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, m->emb_w, m->emb_b,
+                          eps, H, m->x32, m->x16, s));
+    }
+    for (int li = 0; li < c.num_layers; li++) {
+        const DevLayer &L = m->layers[(size_t)li];
+        if ((rc = checkpoint(m, b, cp, s))) return rc;
+        const bool last_cls = cls && li == c.num_layers - 1;
+
+        // qkv = x·Wqkvᵀ + b  (model.go:555)
+        if (q8) {
+            if ((rc = quant(m, m->x32, T, H, H, s))) return rc;
+            rc = gemm(m, K_GEMM_QKV, L.qkv, m->xq, H, m->xs, T, L.qkv_b, nullptr, 0, m->qkv, 3 * H,
+                      fh::ACT_NONE, false, s);
+        } else {
+            rc = gemm(m, K_GEMM_QKV, L.qkv, m->x16, H, nullptr, T, L.qkv_b, nullptr, 0, m->qkv, 3 * H,
+                      fh::ACT_NONE, false, s);
+        }
+        if (rc) return rc;
+
+        // attention (model.go:557-593, 646-701)
+        AttnArgs a{};
+        a.qkv = m->qkv;
+        a.offsets = b.d_offsets;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.out = last_cls ? m->attnc : m->attn;
+        a.H = H;
+        a.d = m->hd;
+        a.ldo = H;
+        a.q_limit = last_cls ? 1 : INT_MAX;
+        a.compact = last_cls ? 1 : 0;
+        a.scale_log2e = (float)(1.0 / std::sqrt((double)m->hd)) * 1.4426950408889634f;
+        {
+            const double nq_l = last_cls ? (double)T : b.sum_l2;  // Σ nq·L
+            Scope sc(m, K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * (q8 ? 4 : 2),
+                     s);
+            LCHK(fh::attention(a, S, b.max_len, q8, s));
+        }
+
+        const int M = last_cls ? S : T;
+        float *xo32 = last_cls ? m->xc32 : m->x32;
+        f16 *xo16 = last_cls ? m->xc16 : m->x16;
+        const void *attn_in = last_cls ? m->attnc : m->attn;
+        if (last_cls) {
+            Scope sc(m, K_GATHER, 0.0, (double)S * H * 8, s);
+            LCHK(fh::gather_rows(m->x32, b.d_offsets, S, H, m->xc32, s));
+        }
+
+        // out projection + bias + residual, norm1 (model.go:596-599)
+        if (q8) {
+            if ((rc = quant(m, (const float *)attn_in, M, H, H, s))) return rc;
+            rc = gemm(m, K_GEMM_OUT, L.out, m->xq, H, m->xs, M, L.out_b, xo32, H, m->y32, H, fh::ACT_NONE, true,
+                      s);
+        } else {
+            rc = gemm(m, K_GEMM_OUT, L.out, attn_in, H, nullptr, M, L.out_b, xo32, H, m->y32, H, fh::ACT_NONE,
+                      true, s);
+        }
+        if (rc) return rc;
+        if ((rc = layer_norm(m, m->y32, M, L.n1w, L.n1b, xo32, xo16, s))) return rc;
+
+        if ((rc = checkpoint(m, b, cp, s))) return rc;
+
+        // FFN (model.go:607-633)
+        const int act = swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU;
+        if (q8) {
+            if ((rc = quant(m, xo32, M, H, H, s))) return rc;
+            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, 0, m->hbuf, I, act, true,
+                           s)))
+                return rc;
+            if ((rc = quant(m, (const float *)m->hbuf, M, I, I, s))) return rc;
+            rc = gemm(m, K_GEMM_FC2, L.fc2, m->xq, I, m->xs, M, L.fc2_b, xo32, H, m->y32, H, fh::ACT_NONE, true, s);
+        } else {
+            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, 0, m->hbuf, I, act,
+                           false, s)))
+                return rc;
+            rc = gemm(m, K_GEMM_FC2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, xo32, H, m->y32, H, fh::ACT_NONE,
+                      true, s);
+        }
+        if (rc) return rc;
+        if ((rc = layer_norm(m, m->y32, M, L.n2w, L.n2b, xo32, xo16, s))) return rc;
+    }
+
+    // pooling → Matryoshka → L2 (model.go:417-453)
+    {
+        const int od = b.out_dim == 0 ? H : b.out_dim;
+        Scope sc(m, K_POOL, 0.0, (cls ? (double)S * H * 4 : (double)T * H * 4) + (double)S * od * 4, s);
+        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, H, cls ? 1 : 0, cls ? 0 : 1,
+                      c.matryoshka_layernorm, od, c.normalize, b.d_out, s));
+    }
+    return FH_OK;
+}
+
+}  // namespace
+
+// ───────────────────────────── C ABI ─────────────────────────────
+
+extern "C" const char *fh_strerror(int code) {
+    switch (code) {
+    case FH_OK: return "ok";
+    case FH_EINVAL: return "invalid argument";
+    case FH_ENOMEM: return "out of memory";
+    case FH_EHIP: return "HIP runtime error";
+    case FH_ECANCELED: return "canceled";
+    case FH_ETOOLONG: return "sequence too long";
+    case FH_ENODEV: return "no gfx950 device";
+    default: return "unknown error";
+    }
+}
+
+extern "C" int fh_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        size_t n = std::min(len - 1, g_err.size());
+        memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return (int)g_err.size();
+}
+
+extern "C" void fh_model_destroy(fh_model *m) {
+    if (!m) return;
+    hipSetDevice(m->device);
+    if (m->stream) hipStreamSynchronize(m->stream);
+    for (auto &p : m->pending) {
+        hipEventDestroy(p.a);
+        hipEventDestroy(p.b);
+    }
+    for (auto e : m->event_pool) hipEventDestroy(e);
+    for (void *p : m->allocs) hipFree(p);
+    if (m->ws) hipFree(m->ws);
+    if (m->pin) hipHostFree(m->pin);
+    if (m->stream) hipStreamDestroy(m->stream);
+    delete m;
+}
+
+extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, int32_t n_tensors, int32_t device,
+                               fh_model **out) {
+    if (!cfg || !out || (n_tensors > 0 && !tensors)) return fail(FH_EINVAL, "fh_model_create: null argument");
+    *out = nullptr;
+    const fh_config &c = *cfg;
+    if (c.hidden_size <= 0 || c.num_layers <= 0 || c.num_heads <= 0 || c.intermediate_size <= 0 ||
+        c.vocab_size <= 0 || c.max_seq_len <= 2 || c.layer_norm_eps <= 0)
+        return fail(FH_EINVAL, "pack: non-positive architecture dimension");
+    if (c.hidden_size % c.num_heads) return fail(FH_EINVAL, "pack: hidden_size not divisible by num_heads");
+    const int H = c.hidden_size, I = c.intermediate_size, hd = H / c.num_heads;
+    // Shape limits of this build's kernels (16-byte vector tiles, LN row in registers).
+    if (H > 1024 || H % 8 || I % 16 || hd % 8 || hd > 128)
+        return fail(FH_EINVAL, "pack: shape H=%d I=%d head_dim=%d outside this build's kernel limits "
+                               "(H ≤ 1024, H%%8 = 0, I%%16 = 0, head_dim%%8 = 0, head_dim ≤ 128)", H, I, hd);
+    if (c.position_encoding == FH_POS_ROPE && c.rope_theta <= 0)
+        return fail(FH_EINVAL, "pack: rope position encoding requires rope_theta > 0");
+
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(FH_ENODEV, "no HIP device visible");
+    if (device < 0 || device >= ndev) return fail(FH_ENODEV, "device %d outside [0,%d)", device, ndev);
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device));
+    if (!strstr(prop.gcnArchName, "gfx950"))
+        return fail(FH_ENODEV, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    HIPCHK(hipSetDevice(device));
+
+    fh_model *m = new fh_model();
+    m->cfg = c;
+    m->device = device;
+    m->hd = hd;
+    m->eff_max = eff_max_len(c);
+    int rc = FH_OK;
+    auto bail = [&](int code) {
+        fh_model_destroy(m);
+        return code;
+    };
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(FH_EHIP, "hipStreamCreate failed"));
+
+    Loader ld{m, tensors, n_tensors, std::vector<bool>((size_t)n_tensors, false)};
+    if ((rc = ld.mat_f32("embeddings.word", c.vocab_size, H, &m->word))) return bail(rc);
+    if (c.position_encoding == FH_POS_ABSOLUTE &&
+        (rc = ld.mat_f32("embeddings.position", c.max_seq_len, H, &m->pos)))
+        return bail(rc);
+    if (c.type_vocab_size > 0) {
+        // Only token type 0 is ever added (model.go:388-390); the table is validated whole.
+        TensorView tv;
+        if ((rc = ld.need("embeddings.token_type", {c.type_vocab_size, H}, tv))) return bail(rc);
+        std::vector<float> t;
+        tv.to_f32(t);
+        if ((rc = upload(m, &m->type0, t.data(), (size_t)H * 4))) return bail(rc);
+    }
+    if ((rc = ld.vec_f32("embeddings.norm.weight", H, &m->emb_w))) return bail(rc);
+    if ((rc = ld.vec_f32("embeddings.norm.bias", H, &m->emb_b))) return bail(rc);
+
+    const bool swiglu = c.activation == FH_ACT_SWIGLU, q8 = c.q8 != 0;
+    m->layers.resize((size_t)c.num_layers);
+    std::vector<float> w, g, packed;
+    for (int li = 0; li < c.num_layers; li++) {
+        DevLayer &L = m->layers[(size_t)li];
+        auto nm = [&](const char *s) { return "layers." + std::to_string(li) + "." + s; };
+        if ((rc = ld.mat_host(nm("attn.qkv.weight"), 3 * H, H, w)) || (rc = upload_mat(m, L.qkv, w, 3 * H, H, q8)))
+            return bail(rc);
+        if ((rc = ld.vec_f32(nm("attn.qkv.bias"), 3 * H, &L.qkv_b, true))) return bail(rc);
+        if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) || (rc = upload_mat(m, L.out, w, H, H, q8)))
+            return bail(rc);
+        if ((rc = ld.vec_f32(nm("attn.out.bias"), H, &L.out_b, true))) return bail(rc);
+        if ((rc = ld.vec_f32(nm("norm1.weight"), H, &L.n1w)) || (rc = ld.vec_f32(nm("norm1.bias"), H, &L.n1b)))
+            return bail(rc);
+        if ((rc = ld.mat_host(nm("mlp.fc1.weight"), I, H, w))) return bail(rc);
+        if (swiglu) {
+            if ((rc = ld.mat_host(nm("mlp.gate.weight"), I, H, g))) return bail(rc);
+            interleave16(w, g, I, H, packed);
+            if ((rc = upload_mat(m, L.ffn1, packed, 2 * I, H, q8))) return bail(rc);
+            // biases follow the same interleave (absent biases stay absent)
+            TensorView tb1, tb2;
+            bool p1 = false, p2 = false;
+            if ((rc = ld.need(nm("mlp.fc1.bias"), {I}, tb1, true, &p1)) ||
+                (rc = ld.need(nm("mlp.gate.bias"), {I}, tb2, true, &p2)))
+                return bail(rc);
+            if (p1 || p2) {
+                std::vector<float> b1((size_t)I, 0.f), b2((size_t)I, 0.f), bp((size_t)2 * I);
+                if (p1) tb1.to_f32(b1);
+                if (p2) tb2.to_f32(b2);
+                for (int r = 0; r < 2 * I; r++) {
+                    const int blk = r / 32, ww = r % 32;
+                    bp[(size_t)r] = ww < 16 ? b1[(size_t)(16 * blk + ww)] : b2[(size_t)(16 * blk + ww - 16)];
+                }
+                if ((rc = upload(m, &L.ffn1_b, bp.data(), bp.size() * 4))) return bail(rc);
+            }
+        } else {
+            if ((rc = upload_mat(m, L.ffn1, w, I, H, q8))) return bail(rc);
+            if ((rc = ld.vec_f32(nm("mlp.fc1.bias"), I, &L.ffn1_b, true))) return bail(rc);
+        }
+        if ((rc = ld.mat_host(nm("mlp.fc2.weight"), H, I, w)) || (rc = upload_mat(m, L.fc2, w, H, I, q8)))
+            return bail(rc);
+        if ((rc = ld.vec_f32(nm("mlp.fc2.bias"), H, &L.fc2_b, true))) return bail(rc);
+        if ((rc = ld.vec_f32(nm("norm2.weight"), H, &L.n2w)) || (rc = ld.vec_f32(nm("norm2.bias"), H, &L.n2b)))
+            return bail(rc);
+    }
+    for (int i = 0; i < n_tensors; i++) {
+        if (!ld.used[(size_t)i])
+            return bail(fail(FH_EINVAL, "pack: unexpected tensor \"%s\" (pack/config mismatch)",
+                             tensors[i].name ? tensors[i].name : "(null)"));
+    }
+    if (c.position_encoding == FH_POS_ROPE) {
+        // native/model.go:306-318: float64 angles, float32 tables, effective max positions.
+        const int half = hd / 2, n = m->eff_max;
+        std::vector<float> cs((size_t)n * half), sn((size_t)n * half);
+        for (int t = 0; t < n; t++)
+            for (int i = 0; i < half; i++) {
+                const double freq = 1.0 / std::pow(c.rope_theta, (double)(2 * i) / (double)hd);
+                const double ang = (double)t * freq;
+                cs[(size_t)t * half + i] = (float)std::cos(ang);
+                sn[(size_t)t * half + i] = (float)std::sin(ang);
+            }
+        if ((rc = upload(m, &m->rope_cos, cs.data(), cs.size() * 4)) ||
+            (rc = upload(m, &m->rope_sin, sn.data(), sn.size() * 4)))
+            return bail(rc);
+    }
+    *out = m;
+    return FH_OK;
+}
+
+extern "C" int64_t fh_model_device_bytes(const fh_model *m) {
+    return m ? m->weight_bytes + (int64_t)m->ws_bytes : 0;
+}
+
+extern "C" int fh_checkpoints_per_call(const fh_model *m) { return m ? 2 * m->cfg.num_layers : 0; }
+
+extern "C" int fh_debug_cancel_after(fh_model *m, int32_t n) {
+    if (!m) return fail(FH_EINVAL, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    m->cancel_after = n;
+    return FH_OK;
+}
+
+extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_offsets, int32_t nseq,
+                         int32_t out_dim, float *out, const volatile int32_t *cancel) {
+    if (!m) return fail(FH_EINVAL, "native: null model");
+    if (nseq < 0) return fail(FH_EINVAL, "native: negative batch size");
+    if (nseq == 0) return FH_OK;
+    if (!ids || !seq_offsets || !out) return fail(FH_EINVAL, "native: null buffer");
+    const fh_config &c = m->cfg;
+    if (seq_offsets[0] != 0) return fail(FH_EINVAL, "native: seq_offsets[0] must be 0");
+    // Per-sequence validation in the reference's order (model.go:348-365).
+    int max_len = 0;
+    double sum_l2 = 0.0;
+    for (int i = 0; i < nseq; i++) {
+        const int L = seq_offsets[i + 1] - seq_offsets[i];
+        if (L <= 0) return fail(FH_EINVAL, "native: batch item %d: native: empty token sequence", i);
+        if (L > m->eff_max)
+            return fail(FH_ETOOLONG,
+                        "native: batch item %d: native: sequence length %d exceeds effective max_seq_len %d "
+                        "(declared %d, trained %d)",
+                        i, L, m->eff_max, c.max_seq_len, c.max_trained_positions);
+        if (out_dim < 0 || out_dim > c.hidden_size)
+            return fail(FH_EINVAL, "native: batch item %d: native: requested dim %d outside [1,%d]", i, out_dim,
+                        c.hidden_size);
+        if (out_dim != 0 && out_dim != c.hidden_size && !c.matryoshka)
+            return fail(FH_EINVAL, "native: batch item %d: native: pack does not support matryoshka truncation to %d",
+                        i, out_dim);
+        for (int t = seq_offsets[i]; t < seq_offsets[i + 1]; t++) {
+            if (ids[t] < 0 || ids[t] >= c.vocab_size)
+                return fail(FH_EINVAL, "native: batch item %d: native: token id %d outside vocab of %d", i, ids[t],
+                            c.vocab_size);
+        }
+        max_len = std::max(max_len, L);
+        sum_l2 += (double)L * L;
+    }
+    const int T = seq_offsets[nseq];
+    const int od = out_dim == 0 ? c.hidden_size : out_dim;
+
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIPCHK(hipSetDevice(m->device));
+    int rc = ensure_workspace(m, T, nseq);
+    if (rc) return rc;
+    const size_t need = align256((size_t)T * 4) + align256((size_t)(nseq + 1) * 4) + (size_t)nseq * od * 4;
+    if (need > m->pin_bytes) {
+        if (m->pin) HIPCHK(hipHostFree(m->pin));
+        m->pin = nullptr;
+        m->pin_bytes = 0;
+        hipError_t e = hipHostMalloc(&m->pin, need, hipHostMallocDefault);
+        if (e != hipSuccess) return fail(FH_ENOMEM, "hipHostMalloc(%zu): %s", need, hipGetErrorString(e));
+        m->pin_bytes = need;
+    }
+    int32_t *p_ids = (int32_t *)m->pin;
+    int32_t *p_off = (int32_t *)((char *)m->pin + align256((size_t)T * 4));
+    float *p_out = (float *)((char *)p_off + align256((size_t)(nseq + 1) * 4));
+    memcpy(p_ids, ids, (size_t)T * 4);
+    memcpy(p_off, seq_offsets, (size_t)(nseq + 1) * 4);
+    HIPCHK(hipMemcpyAsync(m->ids, p_ids, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipMemcpyAsync(m->offsets, p_off, (size_t)(nseq + 1) * 4, hipMemcpyHostToDevice, m->stream));
+    BatchInfo b{m->ids, m->offsets, nseq, T, max_len, out_dim, m->out};
+    b.sum_l2 = sum_l2;
+    b.cancel = cancel;
+    b.host_checks = true;
+    if ((rc = run_forward(m, b, m->stream))) {
+        hipStreamSynchronize(m->stream);
+        return rc;
+    }
+    HIPCHK(hipMemcpyAsync(p_out, m->out, (size_t)nseq * od * 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    memcpy(out, p_out, (size_t)nseq * od * 4);
+    if (m->prof) drain_profile(m);
+    return FH_OK;
+}
+
+extern "C" int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t *d_offsets, int32_t nseq,
+                                int32_t total_tokens, int32_t max_len, int32_t out_dim, float *d_out, void *stream,
+                                const int32_t *h_offsets) {
+    if (!m) return fail(FH_EINVAL, "native: null model");
+    if (nseq <= 0) return nseq == 0 ? FH_OK : fail(FH_EINVAL, "native: negative batch size");
+    if (!d_ids || !d_offsets || !d_out) return fail(FH_EINVAL, "native: null buffer");
+    const fh_config &c = m->cfg;
+    if (out_dim < 0 || out_dim > c.hidden_size || (out_dim != 0 && out_dim != c.hidden_size && !c.matryoshka))
+        return fail(FH_EINVAL, "native: requested dim %d not supported", out_dim);
+    if (max_len <= 0 || max_len > m->eff_max || total_tokens < nseq || total_tokens > (int64_t)nseq * max_len)
+        return fail(FH_EINVAL, "native: inconsistent batch description (T=%d, nseq=%d, max_len=%d)", total_tokens,
+                    nseq, max_len);
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIPCHK(hipSetDevice(m->device));
+    int rc = ensure_workspace(m, total_tokens, nseq);
+    if (rc) return rc;
+    BatchInfo b{d_ids, d_offsets, nseq, total_tokens, max_len, out_dim, d_out};
+    if (h_offsets) {
+        for (int i = 0; i < nseq; i++) {
+            const double L = (double)(h_offsets[i + 1] - h_offsets[i]);
+            b.sum_l2 += L * L;
+        }
+    } else {
+        b.sum_l2 = (double)total_tokens * max_len;  // upper bound without host offsets
+    }
+    return run_forward(m, b, stream ? (hipStream_t)stream : m->stream);
+}
+
+extern "C" int fh_profile_enable(fh_model *m, int32_t on) {
+    if (!m) return fail(FH_EINVAL, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    m->prof = on != 0;
+    return FH_OK;
+}
+
+extern "C" int fh_profile_reset(fh_model *m) {
+    if (!m) return fail(FH_EINVAL, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    drain_profile(m);
+    for (int i = 0; i < K_NCLASS; i++) {
+        m->prof_ms[i] = m->prof_flops[i] = m->prof_bytes[i] = 0.0;
+        m->prof_launches[i] = 0;
+    }
+    return FH_OK;
+}
+
+extern "C" int fh_profile_read(fh_model *m, const char **names, double *ms, int64_t *launches, double *flops,
+                               double *bytes, int32_t cap) {
+    if (!m) return fail(FH_EINVAL, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    drain_profile(m);
+    const int n = std::min<int>(cap, K_NCLASS);
+    for (int i = 0; i < n; i++) {
+        if (names) names[i] = kClassNames[i];
+        if (ms) ms[i] = m->prof_ms[i];
+        if (launches) launches[i] = m->prof_launches[i];
+        if (flops) flops[i] = m->prof_flops[i];
+        if (bytes) bytes[i] = m->prof_bytes[i];
+    }
+    return K_NCLASS;
+}

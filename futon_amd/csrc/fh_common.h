@@ -1,0 +1,68 @@
+// Shared device types and launch plumbing for the futon MI355X (gfx950) encoder.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 64-lane wavefront helpers (CDNA).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Kernel launch parameter blocks.  Every pointer is device memory.
+struct GemmArgs {
+    const void *A;       // [M, K] row-major activations (f16, or i8 codes)
+    const void *B;       // [N, K] row-major weights (nn.Linear layout)
+    const float *bias;   // [N] or null
+    const float *resid;  // [M, ldr] f32 residual added in the epilogue, or null
+    const float *a_scale;  // Q8: [M] per-row activation scales
+    const float *b_scale;  // Q8: [N] per-row weight scales
+    void *C;             // [M, ldc] output (f16 or f32)
+    int M, N, K;
+    int lda, ldb, ldc, ldr;
+};
+
+struct AttnArgs {
+    const f16 *qkv;        // [T, 3H] f16: q | k | v, heads-major inside each
+    const int32_t *offsets;  // [nseq + 1] packed sequence starts
+    const float *rope_cos;   // [maxpos, d/2] or null
+    const float *rope_sin;
+    void *out;             // [T or nseq, ldo]
+    int H, d, ldo;
+    int q_limit;           // queries per sequence that produce output (1 = CLS row)
+    int compact;           // output row = sequence index (CLS mode)
+    float scale_log2e;     // (1/sqrt(d)) * log2(e)
+};
+
+// Host-side launchers (defined next to their kernels).
+namespace fh {
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2 };
+hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
+hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
+hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
+hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
+                    const float *word, const float *type0, const float *pos, const float *gamma,
+                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s);
+hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
+                      float *x32, f16 *x16, hipStream_t s);
+hipError_t gather_rows(const float *x32, const int32_t *offsets, int nseq, int H, float *xc32,
+                       hipStream_t s);
+hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
+                         hipStream_t s);
+hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact,
+                int mean, int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s);
+}  // namespace fh

@@ -1,0 +1,86 @@
+// Per-kernel C entry points (include/futon_hip_ops.h): argument checks,
+// then the same launchers fh_encode uses.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+
+#include "../../include/futon_hip.h"
+#include "../../include/futon_hip_ops.h"
+#include "fh_common.h"
+
+namespace {
+int code_of(hipError_t e) { return e == hipSuccess ? FH_OK : FH_EHIP; }
+}  // namespace
+
+extern "C" int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const float *resid,
+                          const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N, int32_t K,
+                          int32_t act, int32_t out_f32, void *stream) {
+    if (!A || !B || !C || M < 0 || N <= 0 || K <= 0) return FH_EINVAL;
+    if (N % 4 || (act == FH_OP_ACT_SWIGLU && N % 32) || act < 0 || act > 2) return FH_EINVAL;
+    if (dtype == FH_OP_I8 ? (K % 16 || !a_scale || !b_scale) : (dtype != FH_OP_F16 || K % 8)) return FH_EINVAL;
+    GemmArgs g{};
+    g.A = A;
+    g.B = B;
+    g.bias = bias;
+    g.resid = resid;
+    g.a_scale = a_scale;
+    g.b_scale = b_scale;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = K;
+    g.ldb = K;
+    g.ldc = act == FH_OP_ACT_SWIGLU ? N / 2 : N;
+    g.ldr = g.ldc;
+    hipStream_t s = (hipStream_t)stream;
+    return code_of(dtype == FH_OP_I8 ? fh::gemm_i8(g, act, out_f32 != 0, s) : fh::gemm_f16(g, act, out_f32 != 0, s));
+}
+
+extern "C" int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32_t max_len, int32_t H,
+                               int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
+                               int32_t q_limit, int32_t compact, int32_t out_f32, void *stream) {
+    if (!qkv || !offsets || !out || nseq < 0 || max_len <= 0 || heads <= 0 || H % heads) return FH_EINVAL;
+    const int d = H / heads;
+    if (d % 8 || d > 128 || (rope_cos && !rope_sin)) return FH_EINVAL;
+    AttnArgs a{};
+    a.qkv = (const f16 *)qkv;
+    a.offsets = offsets;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.out = out;
+    a.H = H;
+    a.d = d;
+    a.ldo = H;
+    a.q_limit = q_limit > 0 ? q_limit : INT_MAX;
+    a.compact = compact;
+    a.scale_log2e = (float)(1.0 / std::sqrt((double)d)) * 1.4426950408889634f;
+    return code_of(fh::attention(a, nseq, max_len, out_f32 != 0, (hipStream_t)stream));
+}
+
+extern "C" int fh_op_layer_norm(const float *y, int32_t M, int32_t H, const float *gamma, const float *beta, float eps,
+                                float *x32, void *x16, void *stream) {
+    if (!y || !x32 || H <= 0 || H > 1024 || (gamma && !beta)) return FH_EINVAL;
+    return code_of(fh::layer_norm(y, M, H, gamma, beta, eps, x32, (f16 *)x16, (hipStream_t)stream));
+}
+
+extern "C" int fh_op_quantize_rows(const float *x, int32_t M, int32_t K, int8_t *q, float *scale, void *stream) {
+    if (!x || !q || !scale || K <= 0) return FH_EINVAL;
+    return code_of(fh::quantize_rows(x, M, K, K, q, scale, (hipStream_t)stream));
+}
+
+extern "C" int fh_op_embed_ln(const int32_t *ids, const int32_t *offsets, int32_t nseq, int32_t max_len,
+                              const float *word, const float *type0, const float *pos, const float *gamma,
+                              const float *beta, float eps, int32_t H, float *x32, void *x16, void *stream) {
+    if (!ids || !offsets || !word || !gamma || !beta || !x32 || !x16 || H <= 0 || H > 1024) return FH_EINVAL;
+    return code_of(fh::embed_ln(ids, offsets, nseq, max_len, word, type0, pos, gamma, beta, eps, H, x32, (f16 *)x16,
+                                (hipStream_t)stream));
+}
+
+extern "C" int fh_op_pool(const float *x32, const int32_t *offsets, int32_t nseq, int32_t H, int32_t cls_compact,
+                          int32_t matryoshka_ln, int32_t out_dim, int32_t normalize, float *out, void *stream) {
+    if (!x32 || !offsets || !out || H <= 0 || H > 1024 || out_dim <= 0 || out_dim > H) return FH_EINVAL;
+    return code_of(fh::pool(x32, offsets, nseq, H, cls_compact, cls_compact ? 0 : 1, matryoshka_ln, out_dim,
+                            normalize, out, (hipStream_t)stream));
+}

@@ -1,0 +1,232 @@
+// Row-wise, HBM-bound kernels of the encoder forward: embedding gather +
+// LayerNorm, (residual already added) LayerNorm, CLS-row gather, per-row
+// int8 activation quantization, and pooling + Matryoshka + L2.
+//
+// LayerNorm statistics follow native/model.go:743-769: two-pass mean and
+// variance accumulated in float64, inv = float32(1/sqrt(var + eps)),
+// y = (x - float32(mean))·inv·γ + β.  One wavefront per row.
+#include "fh_common.h"
+
+namespace {
+
+constexpr int MAXV = 16;  // values per lane: H ≤ 1024
+
+// LN over v[0..n) held by one wave (element e = lane + 64·j); writes x32/x16 row.
+__device__ __forceinline__ void ln_row(float (&v)[MAXV], int H, const float *gamma,
+                                       const float *beta, float eps, float *o32, f16 *o16) {
+    const int lane = threadIdx.x & 63;
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int e = lane + 64 * j;
+        if (e < H) s += (double)v[j];
+    }
+    const double mean = wave_sum_f64(s) / (double)H;
+    double q = 0.0;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int e = lane + 64 * j;
+        if (e < H) {
+            const double dd = (double)v[j] - mean;
+            q += dd * dd;
+        }
+    }
+    const double var = wave_sum_f64(q) / (double)H;
+    const float inv = (float)(1.0 / sqrt(var + (double)eps));
+    const float mf = (float)mean;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int e = lane + 64 * j;
+        if (e < H) {
+            const float y = gamma ? __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[j], mf), inv), gamma[e]), beta[e])
+                                  : __fmul_rn(__fsub_rn(v[j], mf), inv);
+            if (o32) o32[e] = y;
+            if (o16) o16[e] = (f16)y;
+        }
+    }
+}
+
+// x[t] = LN(word[id_t] + type[0] + pos[t]) — native/model.go:384-396.
+// grid = (ceil(max_len/4), nseq), 4 waves per block, one token per wave.
+__global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t *ids, const int32_t *offsets,
+                                                       const float *word, const float *type0,
+                                                       const float *pos, const float *gamma,
+                                                       const float *beta, float eps, int H,
+                                                       float *x32, f16 *x16) {
+    const int seq = blockIdx.y;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= L) return;
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)(start + t);
+    const float *w = word + (size_t)ids[row] * H;
+    float v[MAXV];
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int e = lane + 64 * j;
+        float x = 0.f;
+        if (e < H) {
+            x = w[e];
+            if (type0) x = __fadd_rn(x, type0[e]);
+            if (pos) x = __fadd_rn(x, pos[(size_t)t * H + e]);
+        }
+        v[j] = x;
+    }
+    ln_row(v, H, gamma, beta, eps, x32 + row * H, x16 + row * H);
+}
+
+// x = LN(y) per row (y already holds proj + bias + residual) — model.go:596-599, 631-633.
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *y, int M, int H,
+                                                         const float *gamma, const float *beta,
+                                                         float eps, float *x32, f16 *x16) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int lane = threadIdx.x & 63;
+    const float *src = y + (size_t)row * H;
+    float v[MAXV];
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < H ? src[e] : 0.f;
+    }
+    ln_row(v, H, gamma, beta, eps, x32 + (size_t)row * H, x16 ? x16 + (size_t)row * H : nullptr);
+}
+
+// xc[i] = x[offsets[i]]: the CLS rows the last layer computes (model.go:403-410).
+__global__ void gather_rows_kernel(const float *x32, const int32_t *offsets, int H, float *xc32) {
+    const int seq = blockIdx.x;
+    const float *src = x32 + (size_t)offsets[seq] * H;
+    for (int e = threadIdx.x; e < H; e += blockDim.x) xc32[(size_t)seq * H + e] = src[e];
+}
+
+// Per-row absmax int8 quantization of activations — native/quant.go:42-70:
+// scale = amax/127 (float32), code = round-half-away(float64(v)·(127/float64(amax))),
+// clamped to ±127; an all-zero row gets scale 0 and zero codes.
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float *x, int M, int K, int ldx,
+                                                            int8_t *q, float *scale) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int lane = threadIdx.x & 63;
+    const float *src = x + (size_t)row * ldx;
+    float amax = 0.f;
+    for (int e = lane; e < K; e += 64) amax = fmaxf(amax, fabsf(src[e]));
+    amax = wave_max(amax);
+    int8_t *dst = q + (size_t)row * K;
+    if (amax == 0.f) {
+        for (int e = lane; e < K; e += 64) dst[e] = 0;
+        if (lane == 0) scale[row] = 0.f;
+        return;
+    }
+    const double inv = 127.0 / (double)amax;
+    for (int e = lane; e < K; e += 64) {
+        double c = round((double)src[e] * inv);
+        c = fmin(127.0, fmax(-127.0, c));
+        dst[e] = (int8_t)c;
+    }
+    if (lane == 0) scale[row] = __fdiv_rn(amax, 127.0f);
+}
+
+__device__ double block_sum_f64(double v, double *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum_f64(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+// Pool → Matryoshka → L2 — native/model.go:417-453.  One block per sequence.
+// CLS reads row seq of the compact last-layer buffer; mean sums the
+// sequence's rows in token order in float32 and scales by float32(1/L).
+__global__ __launch_bounds__(256) void pool_kernel(const float *x32, const int32_t *offsets, int H,
+                                                   int cls_compact, int mean, int mat_ln, int out_dim,
+                                                   int normalize, float *out) {
+    __shared__ float pooled[1024];
+    __shared__ double red[4];
+    const int seq = blockIdx.x;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    for (int e = threadIdx.x; e < H; e += blockDim.x) {
+        float p;
+        if (mean) {
+            p = 0.f;
+            const float *col = x32 + (size_t)start * H + e;
+            for (int t = 0; t < L; ++t) p = __fadd_rn(p, col[(size_t)t * H]);
+            p = __fmul_rn(p, __fdiv_rn(1.0f, (float)L));
+        } else {
+            p = x32[(size_t)(cls_compact ? seq : start) * H + e];
+        }
+        pooled[e] = p;
+    }
+    __syncthreads();
+    int n = H;
+    if (out_dim != H) {
+        if (mat_ln) {
+            double s = 0.0;
+            for (int e = threadIdx.x; e < H; e += blockDim.x) s += (double)pooled[e];
+            const double mu = block_sum_f64(s, red) / (double)H;
+            double q = 0.0;
+            for (int e = threadIdx.x; e < H; e += blockDim.x) {
+                const double dd = (double)pooled[e] - mu;
+                q += dd * dd;
+            }
+            const double var = block_sum_f64(q, red) / (double)H;
+            const float inv = (float)(1.0 / sqrt(var + (double)1e-5f));
+            const float mf = (float)mu;
+            __syncthreads();
+            for (int e = threadIdx.x; e < H; e += blockDim.x)
+                pooled[e] = __fmul_rn(__fsub_rn(pooled[e], mf), inv);
+            __syncthreads();
+        }
+        n = out_dim;
+    }
+    float inv = 1.0f;
+    if (normalize) {
+        double ss = 0.0;
+        for (int e = threadIdx.x; e < n; e += blockDim.x) ss += (double)pooled[e] * (double)pooled[e];
+        ss = block_sum_f64(ss, red);
+        if (ss > 0) inv = (float)(1.0 / sqrt(ss));
+    }
+    for (int e = threadIdx.x; e < n; e += blockDim.x)
+        out[(size_t)seq * n + e] = normalize ? __fmul_rn(pooled[e], inv) : pooled[e];
+}
+
+}  // namespace
+
+namespace fh {
+hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
+                    const float *word, const float *type0, const float *pos, const float *gamma,
+                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s) {
+    if (nseq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_ln_kernel, dim3((max_len + 3) / 4, nseq), dim3(256), 0, s, ids, offsets,
+                       word, type0, pos, gamma, beta, eps, H, x32, x16);
+    return hipGetLastError();
+}
+hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
+                      float *x32, f16 *x16, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, y, M, H, gamma, beta, eps,
+                       x32, x16);
+    return hipGetLastError();
+}
+hipError_t gather_rows(const float *x32, const int32_t *offsets, int nseq, int H, float *xc32,
+                       hipStream_t s) {
+    if (nseq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq), dim3(128), 0, s, x32, offsets, H, xc32);
+    return hipGetLastError();
+}
+hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
+                         hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, M, K, ldx, q, scale);
+    return hipGetLastError();
+}
+hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact, int mean,
+                int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s) {
+    if (nseq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pool_kernel, dim3(nseq), dim3(256), 0, s, x32, offsets, H, cls_compact, mean,
+                       matryoshka_ln, out_dim, normalize, out);
+    return hipGetLastError();
+}
+}  // namespace fh

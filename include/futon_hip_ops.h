@@ -1,0 +1,69 @@
+/*
+ * futon_hip_ops.h — per-kernel C entry points of the gfx950 encoder, on
+ * device pointers.  They expose each kernel that fh_encode chains, so every
+ * step of the forward can be checked in isolation; the GEMM entry is the
+ * device form of the reference's Kernel seam.
+ *
+ * All pointers are device pointers; `stream` is a hipStream_t (NULL = the
+ * null stream).  Calls are asynchronous.  Return FH_OK or FH_E* (see
+ * futon_hip.h); shapes outside a kernel's limits are FH_EINVAL.
+ */
+#ifndef FUTON_HIP_OPS_H
+#define FUTON_HIP_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_OP_F16 0 /* A, B binary16 */
+#define FH_OP_I8 1  /* A, B int8 codes with per-row scales */
+
+#define FH_OP_ACT_NONE 0
+#define FH_OP_ACT_GELU 1
+#define FH_OP_ACT_SWIGLU 2 /* B rows interleaved: 16 fc1 rows, 16 gate rows, … */
+
+/* C[M,N'] = act(A[M,K] · B[N,K]ᵀ (· sA[m]·sB[n] for I8) + bias[N]) + resid[M,N'],
+ * N' = N (N/2 for SwiGLU).  Output f32 when out_f32, else binary16.
+ * Requires K % 16 == 0 for I8, K % 8 == 0 for F16, N % 4 == 0 (N % 32 for SwiGLU).
+ * Replaces: Kernel.MatMulT / MatMulTF16 (native/kernel.go:26-43) and
+ * q8Kernel.MatMulTQ8 (native/quant.go:92-137). */
+int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const float *resid,
+               const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N, int32_t K,
+               int32_t act, int32_t out_f32, void *stream);
+
+/* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
+ * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,
+ * holding each sequence's first q_limit=1 query row), f32 or binary16.
+ * rope_cos/sin: [max_len, head_dim/2] tables or NULL.
+ * Replaces: attendHead + softmaxScaled + rotateHalf (native/model.go:646-739). */
+int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32_t max_len, int32_t H,
+                    int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
+                    int32_t q_limit, int32_t compact, int32_t out_f32, void *stream);
+
+/* x32/x16[M,H] = LN(y) with γ, β (NULL γ = parameter-free).
+ * Replaces: layerNormRows (native/model.go:743-769). */
+int fh_op_layer_norm(const float *y, int32_t M, int32_t H, const float *gamma, const float *beta,
+                     float eps, float *x32, void *x16, void *stream);
+
+/* Per-row int8 codes + scales of x[M,K] (row stride K).
+ * Replaces: quantizeRowQ8 over activation rows (native/quant.go:42-70, :104-110). */
+int fh_op_quantize_rows(const float *x, int32_t M, int32_t K, int8_t *q, float *scale, void *stream);
+
+/* x32/x16[T,H] = LN(word[id] + type0 + pos[t]).  type0/pos may be NULL.
+ * Replaces: the embedding block of EncodeTokensKernel (native/model.go:384-396). */
+int fh_op_embed_ln(const int32_t *ids, const int32_t *offsets, int32_t nseq, int32_t max_len,
+                   const float *word, const float *type0, const float *pos, const float *gamma,
+                   const float *beta, float eps, int32_t H, float *x32, void *x16, void *stream);
+
+/* out[nseq, out_dim] = L2(Matryoshka(pool(x))).  cls_compact: x is [nseq, H]
+ * holding CLS rows; otherwise mean over each sequence's rows of x [T, H].
+ * Replaces: pooling, Matryoshka and L2 of EncodeTokensKernel (native/model.go:417-453). */
+int fh_op_pool(const float *x32, const int32_t *offsets, int32_t nseq, int32_t H, int32_t cls_compact,
+               int32_t matryoshka_ln, int32_t out_dim, int32_t normalize, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FUTON_HIP_OPS_H */

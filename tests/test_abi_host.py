@@ -1,0 +1,172 @@
+"""CPU-side checks of the boundary and the host loader (no GPU compute):
+the library loads and exports every function the public headers declare,
+creation without a gfx950 device fails loudly, and the pack loader rejects
+what the reference's loader rejects (native/model_test.go:479-567,
+native/safetensors_test.go:10-152)."""
+import json
+import os
+import re
+import shutil
+import struct
+
+import numpy as np
+import pytest
+
+import packio
+from futon_amd import _lib, native, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = set()
+    for h in ("futon_hip.h", "futon_hip_ops.h"):
+        src = open(os.path.join(ROOT, "include", h)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        names |= set(re.findall(r"\b(fh_\w+)\s*\(", src))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    declared = header_functions()
+    assert declared == set(_lib.EXPORTED)
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_create_without_device_fails_loudly():
+    cfg, tensors = packio.read_pack(os.path.join(packio.TOY, "toy-absolute-gelu"))
+    try:
+        import torch
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is visible")
+    except ImportError:
+        pass
+    with pytest.raises(_lib.FutonError) as ei:
+        native.Model(native.PackConfig.from_dict(cfg), tensors)
+    assert ei.value.code == _lib.FH_ENODEV
+
+
+def copy_pack(tmp_path, name="toy-absolute-gelu"):
+    dst = tmp_path / name
+    shutil.copytree(os.path.join(packio.TOY, name), dst)
+    return str(dst)
+
+
+def mutate_json(path, fn):
+    d = json.load(open(path))
+    fn(d)
+    open(path, "w").write(json.dumps(d))
+
+
+def rehash(dir):
+    def fn(m):
+        for member in m["members"]:
+            p = os.path.join(dir, member)
+            m["members"][member] = {"sha256": native.sha256_file(p), "size": os.path.getsize(p)}
+    mutate_json(os.path.join(dir, "manifest.json"), fn)
+
+
+def validate_pack(dir):
+    """LoadModel up to (not including) the device upload."""
+    man = native.load_and_verify_manifest(dir)
+    cfg = native.LoadPackConfig(dir)
+    if man["model_id"] != cfg.model_id:
+        raise native.PackError("mixed pack contents")
+    t = native.LoadSafetensorsRaw(os.path.join(dir, "model.safetensors"))
+    native.verify_tensor_names(man, t)
+    return cfg, t
+
+
+def test_toy_packs_validate():
+    for name in ("toy-absolute-gelu", "toy-rope-swiglu"):
+        cfg, t = validate_pack(os.path.join(packio.TOY, name))
+        assert cfg.EffectiveMaxSeqLen() == 64 and len(t) > 10
+
+
+@pytest.mark.parametrize("case", ["wrong_format", "prenorm", "edited_config_stale_manifest", "missing_manifest",
+                                  "truncated_weights", "removed_bias_rehashed", "bad_theta", "bad_matryoshka"])
+def test_pack_tamper_fails_loudly(tmp_path, case):
+    d = copy_pack(tmp_path, "toy-rope-swiglu" if case in ("bad_theta", "bad_matryoshka") else "toy-absolute-gelu")
+    cfgp = os.path.join(d, "config.json")
+    if case == "wrong_format":
+        mutate_json(cfgp, lambda m: m.update(pack_format=99))
+        rehash(d)
+    elif case == "prenorm":
+        mutate_json(cfgp, lambda m: m.update(pre_norm=True))
+        rehash(d)
+    elif case == "edited_config_stale_manifest":
+        mutate_json(cfgp, lambda m: m.update(normalize=False))
+    elif case == "missing_manifest":
+        os.remove(os.path.join(d, "manifest.json"))
+    elif case == "truncated_weights":
+        p = os.path.join(d, "model.safetensors")
+        raw = open(p, "rb").read()
+        open(p, "wb").write(raw[:-100])
+    elif case == "removed_bias_rehashed":
+        p = os.path.join(d, "model.safetensors")
+        t = native.LoadSafetensors(p)
+        del t["layers.0.attn.qkv.bias"]
+        synth.write_safetensors(t, p)
+        rehash(d)
+    elif case == "bad_theta":
+        mutate_json(cfgp, lambda m: m.update(rope_theta=0))
+        rehash(d)
+    elif case == "bad_matryoshka":
+        mutate_json(cfgp, lambda m: m.update(matryoshka={"layernorm": True, "dims": [64]}))
+        rehash(d)
+    with pytest.raises(native.PackError):
+        validate_pack(d)
+
+
+def _st(entries, data):
+    hj = json.dumps(entries).encode()
+    return struct.pack("<Q", len(hj)) + hj + data
+
+
+@pytest.mark.parametrize("raw", [
+    b"\x01\x02",
+    struct.pack("<Q", 1 << 30) + b"{}",
+    _st({"a": {"dtype": "BF16", "shape": [2], "data_offsets": [0, 4]}}, b"\0" * 4),
+    _st({"a": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}, b"\0" * 8),
+    _st({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 12),
+    _st({"a": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8),
+    _st({"a": {"dtype": "F32", "shape": [-1], "data_offsets": [0, 4]}}, b"\0" * 4),
+    _st({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
+         "b": {"dtype": "F32", "shape": [2], "data_offsets": [4, 12]}}, b"\0" * 12),
+    _st({"a": {"dtype": "F32", "shape": [1 << 32, 1 << 32], "data_offsets": [0, 0]}}, b""),
+])
+def test_safetensors_rejects_malformed(raw):
+    with pytest.raises(native.PackError):
+        native.ParseSafetensors(raw)
+
+
+def test_safetensors_round_trip_f16_raw():
+    t = {"w": np.arange(6, dtype=np.float32).reshape(2, 3)}
+    import io
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "m.safetensors")
+        synth.write_safetensors(t, p, "F16")
+        raw = native.LoadSafetensorsRaw(p)
+        assert raw["w"].dtype == np.dtype("<f2")
+        assert np.array_equal(native.LoadSafetensors(p)["w"], t["w"])
+        del io
+
+
+def test_synthetic_pack_is_deterministic(tmp_path):
+    cfg = json.load(open(os.path.join(packio.TOY, "toy-absolute-gelu", "config.json")))
+    a = synth.make_tensors(cfg, 7)
+    b = synth.make_tensors(cfg, 7)
+    for k in a:
+        assert np.array_equal(a[k], b[k])
+    d = synth.write_pack(str(tmp_path / "p"), cfg, a)
+    c2, t2 = validate_pack(d)
+    assert c2.model_id == cfg["model_id"] and set(t2) == set(a)
+    ids, off = synth.make_batch(42, 64, 16, 128)
+    lens = np.diff(off)
+    assert lens.min() >= 16 and lens.max() <= 128
+    assert (ids[off[:-1]] == 101).all() and (ids[off[1:] - 1] == 102).all()
+    inner = np.delete(ids, np.concatenate([off[:-1], off[1:] - 1]))
+    assert inner.min() >= 1000 and inner.max() <= 30521

@@ -1,0 +1,143 @@
+"""End-to-end parity of the GPU forward (fh_encode through the C ABI) with the
+reference's toy goldens and with the oracle, plus the reference's
+behavioural pins: batch ≡ single, determinism, cancellation, rejections."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import packio
+from futon_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+COS_GATE = 0.9999  # every vector vs the reference path
+
+
+def _native():
+    from futon_amd import native
+    return native
+
+
+def toy_model(pack, q8=False):
+    return _native().LoadModel(os.path.join(packio.TOY, pack), q8=q8)
+
+
+@pytest.mark.parametrize("pack", ["toy-absolute-gelu", "toy-rope-swiglu"])
+def test_toy_forward_matches_upstream_goldens(pack):
+    """native/model_test.go:72-97 on the GPU: upstream-generated vectors."""
+    exp = packio.toy_expected()["packs"][pack]
+    m = toy_model(pack)
+    worst = 1.0
+    for c in exp["forward_cases"]:
+        got = m.EncodeTokens(c["ids"])
+        cos = packio.cosine(got, c["vector"])
+        worst = min(worst, cos)
+        assert cos >= COS_GATE, (pack, len(c["ids"]), cos)
+        assert np.abs(got - np.array(c["vector"])).max() < 2e-3
+    for c in exp.get("matryoshka_cases", []):
+        got = m.EncodeTokens(c["ids"], c["dim"])
+        assert got.shape == (c["dim"],)
+        assert packio.cosine(got, c["vector"]) >= COS_GATE
+    print(f"{pack}: min cosine vs upstream {worst:.7f}")
+
+
+@pytest.mark.parametrize("pack", ["toy-absolute-gelu", "toy-rope-swiglu"])
+def test_toy_q8_forward(pack):
+    """native/quant_test.go:152-175 (cos ≥ 0.98 vs upstream) and the oracle's Q8 path at the gate."""
+    exp = packio.toy_expected()["packs"][pack]
+    cfg, tensors = packio.read_pack(os.path.join(packio.TOY, pack))
+    om = oracle.Model(cfg, tensors, q8=True)
+    m = toy_model(pack, q8=True)
+    for c in exp["forward_cases"]:
+        got = m.EncodeTokens(c["ids"])
+        assert packio.cosine(got, c["vector"]) >= 0.98
+        assert packio.cosine(got, om.encode(c["ids"])) >= COS_GATE
+
+
+def test_toy_batch_equals_single_bitwise():
+    """native/model_test.go:165-197: a batched forward is bit-identical to
+    per-sequence forwards, whatever else is in the batch."""
+    m = toy_model("toy-rope-swiglu")
+    rng = np.random.default_rng(3)
+    seqs = [[2] + list(rng.integers(5, 60, n)) + [3] for n in (0, 1, 7, 30, 62, 13)]
+    batch = m.EncodeBatch(seqs)
+    for i, s in enumerate(seqs):
+        single = m.EncodeTokens(s)
+        assert np.array_equal(single.view(np.uint32), batch[i].view(np.uint32)), i
+    # and in another batch order / composition
+    batch2 = m.EncodeBatch(seqs[::-1] + seqs[:2])
+    for i, s in enumerate(seqs[::-1]):
+        assert np.array_equal(batch2[i].view(np.uint32), batch[len(seqs) - 1 - i].view(np.uint32))
+
+
+def test_determinism_repeated_runs():
+    m = toy_model("toy-rope-swiglu")
+    ids = [2, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 3]
+    ref = m.EncodeTokens(ids)
+    for _ in range(3):
+        assert np.array_equal(m.EncodeTokens(ids).view(np.uint32), ref.view(np.uint32))
+
+
+def test_cancellation_at_every_checkpoint():
+    """native/model_test.go:218-244: a cancellation landing on any checkpoint
+    aborts with ECANCELED and no vector."""
+    from futon_amd import _lib
+    m = toy_model("toy-rope-swiglu")
+    ids = [2, 5, 6, 7, 8, 9, 10, 11, 12, 13, 3]
+    total = m.checkpoints_per_call()
+    assert total >= 2 * 2  # per layer + between attention and FFN, 2 layers
+    for n in range(total):
+        m.debug_cancel_after(n)
+        with pytest.raises(_lib.FutonError) as ei:
+            m.EncodeTokens(ids)
+        assert ei.value.code == _lib.FH_ECANCELED
+    m.debug_cancel_after(-1)
+    flag = ctypes.c_int32(1)
+    with pytest.raises(_lib.FutonError) as ei:
+        m.EncodeTokens(ids, cancel=flag)
+    assert ei.value.code == _lib.FH_ECANCELED
+    assert m.EncodeTokens(ids, cancel=ctypes.c_int32(0)).shape == (32,)
+
+
+def test_model_rejects():
+    """native/model_test.go:416-436."""
+    from futon_amd import _lib
+    m = toy_model("toy-absolute-gelu")
+    for ids, dim, code in [([], 0, _lib.FH_EINVAL), ([2, 999, 3], 0, _lib.FH_EINVAL),
+                           ([5] * 65, 0, _lib.FH_ETOOLONG), ([2, 3], 16, _lib.FH_EINVAL),
+                           ([2, 3], 33, _lib.FH_EINVAL), ([2, -1, 3], 0, _lib.FH_EINVAL)]:
+        with pytest.raises(_lib.FutonError) as ei:
+            m.EncodeTokens(ids, dim)
+        assert ei.value.code == code, (ids, dim)
+
+
+def _workload_check(name, batch, max_len=None, len_lo=None, threads=16):
+    w = synth.workload(name)
+    cfg = w.config
+    tensors = synth.make_tensors(cfg, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    lo = len_lo if len_lo is not None else w.len_lo
+    hi = max_len if max_len is not None else w.len_hi
+    ids, offsets = synth.make_batch(w.ids_seed, batch, lo, hi)
+    native = _native()
+    m = native.Model(native.PackConfig.from_dict(cfg), tensors, q8=w.q8)
+    got = m.EncodePacked(ids, offsets, w.out_dim)
+    om = oracle.Model(cfg, tensors, q8=w.q8)
+    want = om.encode_batch(ids, offsets, w.out_dim, threads=threads)
+    cos = [packio.cosine(got[i], want[i]) for i in range(batch)]
+    print(f"{name}: B={batch} min cos {min(cos):.7f} mean {np.mean(cos):.7f}")
+    assert min(cos) >= COS_GATE, (name, int(np.argmin(cos)), min(cos))
+    return m, ids, offsets, got
+
+
+@pytest.mark.parametrize("name,batch,hi,lo", [
+    ("minilm-l6", 8, None, None),
+    ("bge-small", 16, None, None),
+    ("bge-small-q8", 24, None, None),
+    ("bert-base", 2, None, None),
+    ("nomic-bert", 2, 640, 512),
+])
+def test_workload_matches_oracle(name, batch, hi, lo):
+    _workload_check(name, batch, hi, lo)

@@ -1,0 +1,249 @@
+"""Per-kernel parity on the GPU through include/futon_hip_ops.h.
+
+Each kernel is compared with the oracle (or, for the attention core, with a
+float64 restatement of the reference's per-head loop) on identical inputs:
+bit-exact where the arithmetic is integer (Q8 codes and the i8 GEMM), within
+a stated float tolerance elsewhere.  torch is used only to hold device
+memory."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _lib():
+    from futon_amd import _lib
+    return _lib.load()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+def gemm(dtype, A, B, bias=None, resid=None, a_scale=None, b_scale=None, act=0, out_f32=True):
+    M, K = A.shape
+    N = B.shape[0]
+    nout = N // 2 if act == 2 else N
+    C = torch.empty((M, nout), dtype=torch.float32 if out_f32 else torch.float16, device="cuda")
+    rc = _lib().fh_op_gemm(dtype, ptr(A), ptr(B), ptr(bias), ptr(resid), ptr(a_scale), ptr(b_scale), ptr(C),
+                           M, N, K, act, int(out_f32), None)
+    assert rc == 0
+    sync()
+    return C.cpu().numpy()
+
+
+def gelu64(x):
+    from scipy.special import erf
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+
+
+SHAPES = [(1, 4, 8), (3, 32, 32), (37, 96, 64), (130, 256, 384), (300, 1152, 384), (257, 384, 1536),
+          (129, 132, 40)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_f16_matches_float64(M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    b = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64).T + bias
+    got = gemm(0, dev(a), dev(b), dev(bias), dev(resid))
+    # f32 accumulation of exact f16 products: error ≪ 1e-4·sqrt(K)
+    np.testing.assert_allclose(got, ref + resid, atol=2e-4 * math.sqrt(K), rtol=1e-5)
+    got_g = gemm(0, dev(a), dev(b), dev(bias), act=1, out_f32=True)
+    np.testing.assert_allclose(got_g, gelu64(ref), atol=2e-4 * math.sqrt(K), rtol=1e-5)
+    got_h = gemm(0, dev(a), dev(b), None, out_f32=False).astype(np.float64)
+    np.testing.assert_allclose(got_h, ref - bias, atol=2e-3 * math.sqrt(K) / 8, rtol=1e-3)
+
+
+@pytest.mark.parametrize("M,I,K", [(5, 32, 32), (70, 256, 64), (200, 1536, 384)])
+def test_gemm_swiglu_interleave(M, I, K):
+    rng = np.random.default_rng(I + K)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    up = (rng.standard_normal((I, K)) * 0.05).astype(np.float16)
+    gate = (rng.standard_normal((I, K)) * 0.05).astype(np.float16)
+    bu = rng.standard_normal(I).astype(np.float32)
+    bg = rng.standard_normal(I).astype(np.float32)
+    packed = np.empty((2 * I, K), np.float16)
+    pb = np.empty(2 * I, np.float32)
+    for r in range(2 * I):
+        blk, w = divmod(r, 32)
+        src, sb, sr = (up, bu, 16 * blk + w) if w < 16 else (gate, bg, 16 * blk + w - 16)
+        packed[r] = src[sr]
+        pb[r] = sb[sr]
+    u = a.astype(np.float64) @ up.astype(np.float64).T + bu
+    g = a.astype(np.float64) @ gate.astype(np.float64).T + bg
+    ref = u * (g / (1.0 + np.exp(-g)))
+    got = gemm(0, dev(a), dev(packed), dev(pb), act=2, out_f32=True)
+    np.testing.assert_allclose(got, ref, atol=3e-4 * math.sqrt(K), rtol=1e-4)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4, 16), (7, 16, 48), (37, 96, 384), (300, 1152, 384), (65, 384, 1536)])
+def test_q8_quantize_and_gemm_bit_exact(M, N, K):
+    """Activation codes, scales and the i8 GEMM equal the oracle's Q8 path
+    (native/quant.go:42-137) bit for bit."""
+    rng = np.random.default_rng(N + K)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    a[0, :] = 0.0  # all-zero row: scale 0, zero codes
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    qb, sb = oracle.quantize_q8(w)
+    qa_ref = np.zeros((M, K), np.int8)
+    sa_ref = np.zeros(M, np.float32)
+    for i in range(M):
+        qa_ref[i], sa_ref[i] = oracle.quantize_row_q8(a[i])
+    da = dev(a)  # held while the kernels run
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    s = torch.empty(M, dtype=torch.float32, device="cuda")
+    assert _lib().fh_op_quantize_rows(ptr(da), M, K, ptr(q), ptr(s), None) == 0
+    sync()
+    assert np.array_equal(q.cpu().numpy(), qa_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), sa_ref.view(np.uint32))
+    got = gemm(1, q, dev(qb), dev(bias), a_scale=s, b_scale=dev(sb))
+    want = oracle.matmul_t_q8(a, qb, sb, bias)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def attention_ref(qkv, offsets, heads, rope=None, q_limit=None):
+    """float64 restatement of attendHead (native/model.go:646-701) per sequence."""
+    T, H3 = qkv.shape
+    H = H3 // 3
+    d = H // heads
+    x = qkv.astype(np.float64)
+    out = np.zeros((T, H))
+    for s in range(len(offsets) - 1):
+        b, e = offsets[s], offsets[s + 1]
+        L = e - b
+        nq = L if q_limit is None else min(L, q_limit)
+        for h in range(heads):
+            q = x[b:b + nq, h * d:(h + 1) * d].copy()
+            k = x[b:e, H + h * d:H + (h + 1) * d].copy()
+            v = x[b:e, 2 * H + h * d:2 * H + (h + 1) * d]
+            if rope is not None:
+                cos, sin = rope
+                half = d // 2
+                for arr, n in ((q, nq), (k, L)):
+                    c, sn = cos[:n], sin[:n]
+                    x1, x2 = arr[:, :half].copy(), arr[:, half:].copy()
+                    arr[:, :half] = x1 * c - x2 * sn
+                    arr[:, half:] = x2 * c + x1 * sn
+            sc = q @ k.T / math.sqrt(d)
+            sc -= sc.max(axis=1, keepdims=True)
+            p = np.exp(sc)
+            p /= p.sum(axis=1, keepdims=True)
+            out[b:b + nq, h * d:(h + 1) * d] = p @ v
+    return out
+
+
+def rope_tables(n, d, theta):
+    half = d // 2
+    t = np.arange(n, dtype=np.float64)[:, None]
+    freq = 1.0 / theta ** (np.arange(half, dtype=np.float64) * 2 / d)
+    ang = t * freq
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@pytest.mark.parametrize("H,heads,lens,rope", [
+    (32, 4, [1, 2, 9, 33, 64], False),
+    (32, 4, [2, 9, 33, 64], True),
+    (384, 12, [1, 16, 63, 64, 65, 128], False),
+    (768, 12, [512, 77], False),
+    (768, 12, [300, 700], True),
+    (256, 2, [5, 100], False),
+])
+def test_attention_matches_float64(H, heads, lens, rope):
+    rng = np.random.default_rng(H + sum(lens))
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(offsets[-1])
+    qkv = (rng.standard_normal((T, 3 * H)) * 1.5).astype(np.float16)
+    d = H // heads
+    tabs = rope_tables(max(lens), d, 1000.0) if rope else None
+    ref = attention_ref(qkv, offsets, heads, tabs)
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    dc = ds = None
+    if rope:
+        dc, ds = dev(tabs[0]), dev(tabs[1])
+    dq, doff = dev(qkv), dev(offsets)  # held for the kernels' lifetime
+    rc = _lib().fh_op_attention(ptr(dq), ptr(doff), len(lens), max(lens), H, heads, ptr(dc), ptr(ds),
+                                ptr(out), 0, 0, 1, None)
+    assert rc == 0
+    sync()
+    got = out.cpu().numpy()
+    np.testing.assert_allclose(got, ref, atol=3e-3, rtol=3e-3)
+    # CLS-row mode: only query 0 per sequence, written compactly.
+    outc = torch.empty((len(lens), H), dtype=torch.float32, device="cuda")
+    rc = _lib().fh_op_attention(ptr(dq), ptr(doff), len(lens), max(lens), H, heads, ptr(dc), ptr(ds),
+                                ptr(outc), 1, 1, 1, None)
+    assert rc == 0
+    sync()
+    np.testing.assert_allclose(outc.cpu().numpy(), ref[offsets[:-1]], atol=3e-3, rtol=3e-3)
+
+
+@pytest.mark.parametrize("M,H", [(1, 32), (9, 384), (100, 768), (3, 1024)])
+def test_layer_norm_matches_oracle(M, H):
+    rng = np.random.default_rng(M + H)
+    y = (rng.standard_normal((M, H)) * 3 + 0.5).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(H)).astype(np.float32)
+    x32 = torch.empty((M, H), dtype=torch.float32, device="cuda")
+    x16 = torch.empty((M, H), dtype=torch.float16, device="cuda")
+    dy, dg, db = dev(y), dev(g), dev(b)
+    assert _lib().fh_op_layer_norm(ptr(dy), M, H, ptr(dg), ptr(db), 1e-12, ptr(x32), ptr(x16), None) == 0
+    sync()
+    want = oracle.layer_norm_rows(y, g, b, 1e-12)
+    np.testing.assert_allclose(x32.cpu().numpy(), want, atol=2e-6, rtol=0)
+    np.testing.assert_allclose(x16.cpu().numpy().astype(np.float32), want, atol=4e-3, rtol=1e-3)
+
+
+def test_embed_ln_and_pool():
+    rng = np.random.default_rng(5)
+    H, V = 64, 50
+    lens = [1, 3, 17]
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(offsets[-1])
+    ids = rng.integers(0, V, T).astype(np.int32)
+    word = rng.standard_normal((V, H)).astype(np.float32)
+    typ = rng.standard_normal(H).astype(np.float32)
+    pos = rng.standard_normal((32, H)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    x32 = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    x16 = torch.empty((T, H), dtype=torch.float16, device="cuda")
+    d_in = [dev(a) for a in (ids, offsets, word, typ, pos, g, b)]
+    rc = _lib().fh_op_embed_ln(ptr(d_in[0]), ptr(d_in[1]), len(lens), max(lens), ptr(d_in[2]), ptr(d_in[3]),
+                               ptr(d_in[4]), ptr(d_in[5]), ptr(d_in[6]), 1e-12, H, ptr(x32), ptr(x16), None)
+    assert rc == 0
+    sync()
+    rows = []
+    for s in range(len(lens)):
+        for t in range(lens[s]):
+            rows.append(word[ids[offsets[s] + t]] + typ + pos[t])
+    want = oracle.layer_norm_rows(np.array(rows, np.float32), g, b, 1e-12)
+    np.testing.assert_allclose(x32.cpu().numpy(), want, atol=2e-6, rtol=0)
+
+    # mean pool + Matryoshka LN + L2 over the same rows
+    out = torch.empty((len(lens), 16), dtype=torch.float32, device="cuda")
+    assert _lib().fh_op_pool(ptr(x32), ptr(d_in[1]), len(lens), H, 0, 1, 16, 1, ptr(out), None) == 0
+    sync()
+    exp = []
+    for s in range(len(lens)):
+        p = want[offsets[s]:offsets[s + 1]].sum(axis=0, dtype=np.float32) * np.float32(1.0 / lens[s])
+        p = oracle.layer_norm_rows(p, None, None, 1e-5)[0][:16].astype(np.float64)
+        exp.append(p / np.sqrt((p * p).sum()))
+    np.testing.assert_allclose(out.cpu().numpy(), np.array(exp), atol=2e-6, rtol=0)
