@@ -427,13 +427,14 @@ int checkpoint(fh_model *m, const BatchInfo &b, int &cp, hipStream_t s) {
 }
 
 int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const float *a_scale, int M,
-         const float *bias, const float *resid, int ldr, void *C, int ldc, int act, bool out_f32,
-         hipStream_t s) {
+         const float *bias, const float *resid, const f16 *resid_h, int ldr, void *C, int ldc, int act,
+         bool out_f32, hipStream_t s) {
     GemmArgs g{};
     g.A = A;
     g.B = w.w;
     g.bias = bias;
     g.resid = resid;
+    g.resid_h = resid_h;
     g.a_scale = a_scale;
     g.b_scale = w.scale;
     g.C = C;
@@ -448,7 +449,7 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     const double flops = 2.0 * M * (double)w.n * w.k;
     const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
     const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
-                         (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : 0.0);
+                         (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : resid_h ? (double)M * outn * 2 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
     LCHK(i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
     return FH_OK;
@@ -463,7 +464,7 @@ int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s) {
 int layer_norm(fh_model *m, const float *y, int M, const float *gw, const float *gb, float *x32, f16 *x16,
                hipStream_t s) {
     const int H = m->cfg.hidden_size;
-    Scope sc(m, K_LN, 0.0, (double)M * H * (4 + 4 + 2), s);
+    Scope sc(m, K_LN, 0.0, (double)M * H * (4 + (x32 ? 4 : 0) + 2), s);
     LCHK(fh::layer_norm(y, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
     return FH_OK;
 }
@@ -473,25 +474,30 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
     const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
     const bool q8 = c.q8 != 0, cls = c.pooling == FH_POOL_CLS, swiglu = c.activation == FH_ACT_SWIGLU;
     const float eps = (float)c.layer_norm_eps;
+    // Residual stream: binary16 between layers (the GEMM epilogues add it in
+    // f32), except on the Q8 path, whose activation quantizer reads the f32
+    // stream like quant.go:104-110.  The last layer's LN always writes f32
+    // for pooling.
+    const bool f32res = q8;
     int cp = 0, rc;
 
     {
-        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + 6) + T * 4.0, s);
+        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + (f32res ? 6 : 2)) + T * 4.0, s);
         LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, m->emb_w, m->emb_b,
-                          eps, H, m->x32, m->x16, s));
+                          eps, H, f32res ? m->x32 : nullptr, m->x16, s));
     }
     for (int li = 0; li < c.num_layers; li++) {
         const DevLayer &L = m->layers[(size_t)li];
         if ((rc = checkpoint(m, b, cp, s))) return rc;
-        const bool last_cls = cls && li == c.num_layers - 1;
+        const bool last = li == c.num_layers - 1, last_cls = cls && last;
 
         // qkv = x·Wqkvᵀ + b  (model.go:555)
         if (q8) {
             if ((rc = quant(m, m->x32, T, H, H, s))) return rc;
-            rc = gemm(m, K_GEMM_QKV, L.qkv, m->xq, H, m->xs, T, L.qkv_b, nullptr, 0, m->qkv, 3 * H,
+            rc = gemm(m, K_GEMM_QKV, L.qkv, m->xq, H, m->xs, T, L.qkv_b, nullptr, nullptr, 0, m->qkv, 3 * H,
                       fh::ACT_NONE, false, s);
         } else {
-            rc = gemm(m, K_GEMM_QKV, L.qkv, m->x16, H, nullptr, T, L.qkv_b, nullptr, 0, m->qkv, 3 * H,
+            rc = gemm(m, K_GEMM_QKV, L.qkv, m->x16, H, nullptr, T, L.qkv_b, nullptr, nullptr, 0, m->qkv, 3 * H,
                       fh::ACT_NONE, false, s);
         }
         if (rc) return rc;
@@ -521,21 +527,24 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         f16 *xo16 = last_cls ? m->xc16 : m->x16;
         const void *attn_in = last_cls ? m->attnc : m->attn;
         if (last_cls) {
-            Scope sc(m, K_GATHER, 0.0, (double)S * H * 8, s);
-            LCHK(fh::gather_rows(m->x32, b.d_offsets, S, H, m->xc32, s));
+            Scope sc(m, K_GATHER, 0.0, (double)S * H * (f32res ? 8 : 4), s);
+            LCHK(fh::gather_rows(f32res ? m->x32 : nullptr, f32res ? nullptr : m->x16, b.d_offsets, S, H,
+                                 f32res ? m->xc32 : nullptr, f32res ? nullptr : m->xc16, s));
         }
+        const float *r32 = f32res ? xo32 : nullptr;
+        const f16 *r16 = f32res ? nullptr : xo16;
 
         // out projection + bias + residual, norm1 (model.go:596-599)
         if (q8) {
             if ((rc = quant(m, (const float *)attn_in, M, H, H, s))) return rc;
-            rc = gemm(m, K_GEMM_OUT, L.out, m->xq, H, m->xs, M, L.out_b, xo32, H, m->y32, H, fh::ACT_NONE, true,
-                      s);
+            rc = gemm(m, K_GEMM_OUT, L.out, m->xq, H, m->xs, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
+                      true, s);
         } else {
-            rc = gemm(m, K_GEMM_OUT, L.out, attn_in, H, nullptr, M, L.out_b, xo32, H, m->y32, H, fh::ACT_NONE,
+            rc = gemm(m, K_GEMM_OUT, L.out, attn_in, H, nullptr, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, m->y32, M, L.n1w, L.n1b, xo32, xo16, s))) return rc;
+        if ((rc = layer_norm(m, m->y32, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
 
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
@@ -543,20 +552,21 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int act = swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU;
         if (q8) {
             if ((rc = quant(m, xo32, M, H, H, s))) return rc;
-            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, 0, m->hbuf, I, act, true,
-                           s)))
+            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
+                           act, true, s)))
                 return rc;
             if ((rc = quant(m, (const float *)m->hbuf, M, I, I, s))) return rc;
-            rc = gemm(m, K_GEMM_FC2, L.fc2, m->xq, I, m->xs, M, L.fc2_b, xo32, H, m->y32, H, fh::ACT_NONE, true, s);
+            rc = gemm(m, K_GEMM_FC2, L.fc2, m->xq, I, m->xs, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE, true,
+                      s);
         } else {
-            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, 0, m->hbuf, I, act,
-                           false, s)))
+            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
+                           act, false, s)))
                 return rc;
-            rc = gemm(m, K_GEMM_FC2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, xo32, H, m->y32, H, fh::ACT_NONE,
+            rc = gemm(m, K_GEMM_FC2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, m->y32, M, L.n2w, L.n2b, xo32, xo16, s))) return rc;
+        if ((rc = layer_norm(m, m->y32, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
     }
 
     // pooling → Matryoshka → L2 (model.go:417-453)

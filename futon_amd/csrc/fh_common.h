@@ -29,11 +29,13 @@ struct GemmArgs {
     const void *B;       // [N, K] row-major weights (nn.Linear layout)
     const float *bias;   // [N] or null
     const float *resid;  // [M, ldr] f32 residual added in the epilogue, or null
+    const f16 *resid_h;  // [M, ldr] f16 residual (used when resid is null), or null
     const float *a_scale;  // Q8: [M] per-row activation scales
     const float *b_scale;  // Q8: [N] per-row weight scales
     void *C;             // [M, ldc] output (f16 or f32)
     int M, N, K;
     int lda, ldb, ldc, ldr;
+    int epi_lds;         // set by the launcher: stage the epilogue through LDS
 };
 
 struct AttnArgs {
@@ -59,8 +61,8 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s);
 hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
                       float *x32, f16 *x16, hipStream_t s);
-hipError_t gather_rows(const float *x32, const int32_t *offsets, int nseq, int H, float *xc32,
-                       hipStream_t s);
+hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,
+                       f16 *xc16, hipStream_t s);
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
                          hipStream_t s);
 hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact,

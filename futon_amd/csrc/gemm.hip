@@ -9,26 +9,64 @@
 // v_mfma_i32_16x16x64_i8, exact i32 accumulate, epilogue
 // float(sum)·(sA·sB) + bias evaluated unfused as in quant.go:129-133.
 //
-// Tiling: 128×128 block tile, 256 threads = 4 waves in 2×2, 64×64 per wave
-// (4×4 MFMA tiles), 64-element (f16) / 128-byte (i8) K slices staged
-// through double-buffered LDS with one barrier per K slice.  The MFMA is
-// issued with the weight fragment as the A operand, so each lane ends up
-// holding four consecutive output columns of one row: epilogue stores are
-// 8/16-byte vectors, and the SwiGLU up/gate pair (interleaved in 16-row
-// blocks at load) lands in the same lane.
+// Tiling (template Cfg): BM×BN block tile, WM×WN waves each owning a
+// (BM/WM)×(BN/WN) tile of 16×16 MFMA tiles, 128-byte K slices (64 f16 or
+// 128 i8) staged through double-buffered LDS with one barrier per slice;
+// the next slice's global loads are in flight while the current one is
+// multiplied.  The MFMA is issued with the weight fragment as the A
+// operand, so each lane ends up holding four consecutive output columns of
+// one row: epilogue stores are 8/16-byte vectors, and the SwiGLU up/gate
+// pair (interleaved in 16-row blocks at load) lands in the same lane.
+#include <cstdlib>
+
 #include "fh_common.h"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, NT = 256;
-constexpr int KB = 128;            // bytes of K per slice (64 f16 or 128 i8)
-constexpr int LDS_ROW = KB + 16;   // bytes; +16 staggers rows across LDS banks
+constexpr int KB = 128;  // bytes of K per slice (64 f16 or 128 i8)
 
+// PAD: bytes appended to each 128-byte LDS row (the row stride decides the
+// ds_read_b128 bank pattern); PF: register prefetch depth in slices (1 or 2).
+template <int BM_, int BN_, int WM_, int WN_, int PAD_, int PF_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PF = PF_;
+    static constexpr int ROW = KB + PAD_;
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int MT = BM / WM / 16;  // 16-row MFMA tiles per wave
+    static constexpr int NTL = BN / WN / 16; // 16-col MFMA tiles per wave
+    static constexpr int ACH = BM * (KB / 16) / NT;  // 16-byte A chunks per thread per slice
+    static constexpr int BCH = BN * (KB / 16) / NT;
+    static_assert(ACH * NT == BM * (KB / 16) && BCH * NT == BN * (KB / 16), "tile/thread mismatch");
+};
+
+// erf-GELU, 0.5·x·(1 + erf(x/√2)), through the branch-free Numerical Recipes
+// erfc fit the reference uses (native/mathf32.go:73-107; fractional error
+// < 1.2e-7), with the hardware exp.
 __device__ __forceinline__ float gelu_erf(float x) {
-    // 0.5·x·(1 + erf(x/√2)) written through erfc so both tails stay accurate.
-    return 0.5f * x * erfcf(-x * 0.70710678118654752f);
+    const float a = fabsf(x) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.5f * a);
+    float p = 0.17087277f;
+    p = p * t - 0.82215223f;
+    p = p * t + 1.48851587f;
+    p = p * t - 1.13520398f;
+    p = p * t + 0.27886807f;
+    p = p * t - 0.18628806f;
+    p = p * t + 0.09678418f;
+    p = p * t + 0.37409196f;
+    p = p * t + 1.00002368f;
+    p = p * t - 1.26551223f;
+    const float c = t * __expf(p - a * a);  // erfc(|x|/√2)
+    return x < 0.f ? 0.5f * x * c : 0.5f * x * (2.0f - c);
 }
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences
+// global memory, which makes every barrier wait for all in-flight global
+// loads and so cancels the prefetch of the next slices; the K loop only
+// needs this wave's LDS reads and writes complete before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // Maps the hardware block id onto (m-tile, n-tile) so that each of the 8
 // XCDs (which receive block ids round-robin) works on a contiguous range of
@@ -50,10 +88,8 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
         // col is the packed up-column; output column folds the 16-row interleave.
         const int ocol = ((col >> 5) << 4) + (col & 15);
         if (g.bias) {
-            const f32x4 bu = *(const f32x4 *)(g.bias + col);
-            const f32x4 bg = *(const f32x4 *)(g.bias + col + 16);
-            v += bu;
-            gate += bg;
+            v += *(const f32x4 *)(g.bias + col);
+            gate += *(const f32x4 *)(g.bias + col + 16);
         }
         f32x4 o;
 #pragma unroll
@@ -71,7 +107,12 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
     }
-    if (g.resid) v += *(const f32x4 *)(g.resid + (size_t)row * g.ldr + col);
+    if (g.resid) {
+        v += *(const f32x4 *)(g.resid + (size_t)row * g.ldr + col);
+    } else if (g.resid_h) {
+        const f16x4 r = *(const f16x4 *)(g.resid_h + (size_t)row * g.ldr + col);
+        v += (f32x4){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+    }
     if (OUT_F32) {
         *(f32x4 *)((float *)g.C + (size_t)row * g.ldc + col) = v;
     } else {
@@ -80,108 +121,27 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
     }
 }
 
-// One kernel body for both element types.  ELT = bytes per element of A/B.
-template <bool I8, int ACT, bool OUT_F32>
-__global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) uint8_t As[2][BM * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * LDS_ROW];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    int mt, nt;
-    tile_coords(mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-    constexpr int ESZ = I8 ? 1 : 2;
-    const int kbytes = g.K * ESZ;
-    const uint8_t *A = (const uint8_t *)g.A;
-    const uint8_t *B = (const uint8_t *)g.B;
-    const size_t lda = (size_t)g.lda * ESZ, ldb = (size_t)g.ldb * ESZ;
-
-    // Each thread moves 4 sixteen-byte chunks of A and of B per K slice:
-    // chunk c = tid + i·256 covers row c/8, bytes (c%8)·16 of the slice.
-    i32x4 ra[4], rb[4];
-    const i32x4 zero = {0, 0, 0, 0};
-    auto gload = [&](int kb0) {
+// Epilogue over a wave's tiles.  Lane holds C[row][col .. col+3] for
+// row = tile_m + lane%16, col = tile_n + (lane/16)·4.
+template <class C, bool I8, int ACT, bool OUT_F32>
+__device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
+                                            const f32x4 (&acc)[C::NTL][C::MT], const i32x4 (&iacc)[C::NTL][C::MT]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * NT, r = c >> 3, kb = kb0 + (c & 7) * 16;
-            const int ar = min(m0 + r, g.M - 1), br = min(n0 + r, g.N - 1);
-            ra[i] = kb < kbytes ? *(const i32x4 *)(A + ar * lda + kb) : zero;
-            rb[i] = kb < kbytes ? *(const i32x4 *)(B + br * ldb + kb) : zero;
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * NT, r = c >> 3, cb = (c & 7) * 16;
-            *(i32x4 *)&As[buf][r * LDS_ROW + cb] = ra[i];
-            *(i32x4 *)&Bs[buf][r * LDS_ROW + cb] = rb[i];
-        }
-    };
-
-    f32x4 acc[4][4];
-    i32x4 iacc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            iacc[a][b] = zero;
-        }
-
-    const int nk = (kbytes + KB - 1) / KB;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * KB);
-#pragma unroll
-        for (int kk = 0; kk < KB; kk += 64) {  // 64 bytes of K per MFMA step
-            i32x4 af[4], bf[4];
-            const int kofs = kk + (lane >> 4) * 16;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                af[t] = *(const i32x4 *)&As[cur][(wm * 64 + t * 16 + (lane & 15)) * LDS_ROW + kofs];
-                bf[t] = *(const i32x4 *)&Bs[cur][(wn * 64 + t * 16 + (lane & 15)) * LDS_ROW + kofs];
-            }
-#pragma unroll
-            for (int tn = 0; tn < 4; ++tn)
-#pragma unroll
-                for (int tm = 0; tm < 4; ++tm) {
-                    if (I8) {
-                        iacc[tn][tm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[tn], af[tm], iacc[tn][tm],
-                                                                            0, 0, 0);
-                    } else {
-                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[tm]),
-                            acc[tn][tm], 0, 0, 0);
-                    }
-                }
-        }
-        if (kt + 1 < nk) sstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    // Lane holds C[row][col .. col+3] for row = tile_m + lane%16,
-    // col = tile_n + (lane/16)·4.
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-        const int row = m0 + wm * 64 + tm * 16 + (lane & 15);
+    for (int tm = 0; tm < C::MT; ++tm) {
+        const int row = m0 + (wm * C::MT + tm) * 16 + (lane & 15);
         if (row >= g.M) continue;
         float sa = 0.f;
         if (I8) sa = g.a_scale[row];
 #pragma unroll
-        for (int tn = 0; tn < 4; ++tn) {
+        for (int tn = 0; tn < C::NTL; ++tn) {
             if (ACT == fh::ACT_SWIGLU && (tn & 1)) continue;
-            const int col = n0 + wn * 64 + tn * 16 + (lane >> 4) * 4;
+            const int col = n0 + (wn * C::NTL + tn) * 16 + (lane >> 4) * 4;
             if (col >= g.N) continue;
             f32x4 v, gate = {0.f, 0.f, 0.f, 0.f};
             if (I8) {
                 const f32x4 sb = *(const f32x4 *)(g.b_scale + col);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    v[i] = __fmul_rn((float)iacc[tn][tm][i], __fmul_rn(sa, sb[i]));
+                for (int i = 0; i < 4; ++i) v[i] = __fmul_rn((float)iacc[tn][tm][i], __fmul_rn(sa, sb[i]));
                 if (ACT == fh::ACT_SWIGLU) {
                     const f32x4 sg = *(const f32x4 *)(g.b_scale + col + 16);
 #pragma unroll
@@ -197,24 +157,438 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     }
 }
 
-template <bool I8>
-hipError_t launch(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
-    if (g.M <= 0) return hipSuccess;
-    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
-    dim3 block(NT);
-#define FH_GEMM_CASE(ACTV, F32)                                                              \
-    if (act == ACTV && out_f32 == F32) {                                                    \
-        hipLaunchKernelGGL((gemm_kernel<I8, ACTV, F32>), grid, block, 0, s, g);            \
-        return hipGetLastError();                                                           \
+// Epilogue through LDS.  A lane's MFMA results are four columns of one row,
+// so storing them directly writes 16 rows × 32 bytes per instruction.  Here
+// each wave stages 32 rows of its (after bias/activation/scales) tile in its
+// own LDS region, then writes whole row segments with 16-byte stores, adding
+// the residual in the same coalesced pass.  Needs 64 output columns per wave
+// (32 for SwiGLU) and the operand LDS free (after the K loop's last barrier).
+template <class C, bool I8, int ACT, bool OUT_F32>
+__device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
+                                                int wave, const f32x4 (&acc)[C::NTL][C::MT],
+                                                const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds) {
+    static_assert(C::NTL * 16 == 64 && C::MT % 2 == 0, "staged epilogue expects 64-column wave tiles");
+    constexpr int OC = ACT == fh::ACT_SWIGLU ? 32 : 64;  // output columns per wave
+    constexpr int ESZ = OUT_F32 ? 4 : 2;
+    constexpr int RS = OC * ESZ + 16;                    // LDS row stride (bytes)
+    constexpr int CPR = OC * ESZ / 16;                   // 16-byte chunks per row
+    uint8_t *region = lds + wave * 32 * RS;
+    const int ocol0 = ACT == fh::ACT_SWIGLU ? (n0 + wn * 64) >> 1 : n0 + wn * 64;
+#pragma unroll
+    for (int p = 0; p < C::MT / 2; ++p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int tm = 2 * p + h;
+            const int row = m0 + (wm * C::MT + tm) * 16 + (lane & 15);
+            float sa = 0.f;
+            if (I8) sa = g.a_scale[min(row, g.M - 1)];
+#pragma unroll
+            for (int tn = 0; tn < C::NTL; ++tn) {
+                if (ACT == fh::ACT_SWIGLU && (tn & 1)) continue;
+                const int col = n0 + (wn * C::NTL + tn) * 16 + (lane >> 4) * 4;
+                f32x4 v, gate = {0.f, 0.f, 0.f, 0.f};
+                if (I8) {
+                    const f32x4 sb = *(const f32x4 *)(g.b_scale + col);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = __fmul_rn((float)iacc[tn][tm][i], __fmul_rn(sa, sb[i]));
+                    if (ACT == fh::ACT_SWIGLU) {
+                        const f32x4 sg = *(const f32x4 *)(g.b_scale + col + 16);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            gate[i] = __fmul_rn((float)iacc[tn + 1][tm][i], __fmul_rn(sa, sg[i]));
+                    }
+                } else {
+                    v = acc[tn][tm];
+                    if (ACT == fh::ACT_SWIGLU) gate = acc[tn + 1][tm];
+                }
+                if (ACT == fh::ACT_SWIGLU) {
+                    if (g.bias) {
+                        v += *(const f32x4 *)(g.bias + col);
+                        gate += *(const f32x4 *)(g.bias + col + 16);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = v[i] * silu(gate[i]);
+                } else {
+                    if (g.bias) v += *(const f32x4 *)(g.bias + col);
+                    if (ACT == fh::ACT_GELU) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
+                    }
+                }
+                const int lc = (ACT == fh::ACT_SWIGLU ? (tn >> 1) : tn) * 16 + (lane >> 4) * 4;
+                uint8_t *dst = region + (h * 16 + (lane & 15)) * RS + lc * ESZ;
+                if (OUT_F32) {
+                    *(f32x4 *)dst = v;
+                } else {
+                    *(f16x4 *)dst = (f16x4){(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                }
+            }
+        }
+        // Same-wave LDS accesses complete in order: the rows are readable now.
+#pragma unroll
+        for (int j = 0; j < 32 * CPR / 64; ++j) {
+            const int c = lane + 64 * j, r = c / CPR, ch = c % CPR;
+            const int grow = m0 + (wm * C::MT + 2 * p) * 16 + r;
+            i32x4 d = *(const i32x4 *)(region + r * RS + ch * 16);
+            if (grow >= g.M) continue;
+            const int gcol = ocol0 + ch * (16 / ESZ);
+            if (OUT_F32 && (g.resid || g.resid_h)) {
+                f32x4 v = __builtin_bit_cast(f32x4, d);
+                if (g.resid) {
+                    v += *(const f32x4 *)(g.resid + (size_t)grow * g.ldr + gcol);
+                } else {
+                    const f16x4 rr = *(const f16x4 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                    v += (f32x4){(float)rr[0], (float)rr[1], (float)rr[2], (float)rr[3]};
+                }
+                d = __builtin_bit_cast(i32x4, v);
+            }
+            *(i32x4 *)((uint8_t *)g.C + ((size_t)grow * g.ldc + gcol) * ESZ) = d;
+        }
     }
-    FH_GEMM_CASE(fh::ACT_NONE, false)
-    FH_GEMM_CASE(fh::ACT_NONE, true)
-    FH_GEMM_CASE(fh::ACT_GELU, false)
-    FH_GEMM_CASE(fh::ACT_GELU, true)
-    FH_GEMM_CASE(fh::ACT_SWIGLU, false)
-    FH_GEMM_CASE(fh::ACT_SWIGLU, true)
-#undef FH_GEMM_CASE
-    return hipErrorInvalidValue;
+}
+
+template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32>
+__global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][C::BM * C::ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    int mt, nt;
+    tile_coords(mt, nt);
+    const int m0 = mt * C::BM, n0 = nt * C::BN;
+    constexpr int ESZ = I8 ? 1 : 2;
+    const int kbytes = g.K * ESZ;
+    const uint8_t *A = (const uint8_t *)g.A;
+    const uint8_t *B = (const uint8_t *)g.B;
+    const size_t lda = (size_t)g.lda * ESZ, ldb = (size_t)g.ldb * ESZ;
+    const i32x4 zero = {0, 0, 0, 0};
+
+    // Per-thread source rows (clamped into the matrix; clamped rows are
+    // computed and never stored) for chunk c = tid + i·NT: row c/8, bytes (c%8)·16.
+    const uint8_t *asrc[C::ACH];
+    const uint8_t *bsrc[C::BCH];
+#pragma unroll
+    for (int i = 0; i < C::ACH; ++i) {
+        const int c = tid + i * C::NT;
+        asrc[i] = A + (size_t)min(m0 + (c >> 3), g.M - 1) * lda + (c & 7) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::BCH; ++i) {
+        const int c = tid + i * C::NT;
+        bsrc[i] = B + (size_t)min(n0 + (c >> 3), g.N - 1) * ldb + (c & 7) * 16;
+    }
+
+    // Two register stages: slice k+2 is fetched while slice k is multiplied
+    // and slice k+1 waits in registers, so ~two slices of MFMA work cover the
+    // global-load latency.
+    i32x4 ra[C::PF][C::ACH], rb[C::PF][C::BCH];
+    auto gload = [&](int st, int kb0) {
+#pragma unroll
+        for (int i = 0; i < C::ACH; ++i) {
+            if (KFULL) {
+                ra[st][i] = *(const i32x4 *)(asrc[i] + kb0);
+            } else {
+                const int kb = kb0 + ((tid + i * C::NT) & 7) * 16;
+                ra[st][i] = kb < kbytes ? *(const i32x4 *)(asrc[i] + kb0) : zero;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::BCH; ++i) {
+            if (KFULL) {
+                rb[st][i] = *(const i32x4 *)(bsrc[i] + kb0);
+            } else {
+                const int kb = kb0 + ((tid + i * C::NT) & 7) * 16;
+                rb[st][i] = kb < kbytes ? *(const i32x4 *)(bsrc[i] + kb0) : zero;
+            }
+        }
+    };
+    auto sstore = [&](int st, int buf) {
+#pragma unroll
+        for (int i = 0; i < C::ACH; ++i) {
+            const int c = tid + i * C::NT;
+            *(i32x4 *)&As[buf][(c >> 3) * C::ROW + (c & 7) * 16] = ra[st][i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::BCH; ++i) {
+            const int c = tid + i * C::NT;
+            *(i32x4 *)&Bs[buf][(c >> 3) * C::ROW + (c & 7) * 16] = rb[st][i];
+        }
+    };
+
+    f32x4 acc[C::NTL][C::MT];
+    i32x4 iacc[C::NTL][C::MT];
+#pragma unroll
+    for (int a = 0; a < C::NTL; ++a)
+#pragma unroll
+        for (int b = 0; b < C::MT; ++b) {
+            acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            iacc[a][b] = zero;
+        }
+
+    const int nk = (kbytes + KB - 1) / KB;
+    const int arow0 = (wm * C::MT * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
+    const int brow0 = (wn * C::NTL * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
+    auto compute = [&](int cur) {
+#pragma unroll
+        for (int kk = 0; kk < KB; kk += 64) {  // 64 bytes of K per MFMA step
+            i32x4 af[C::MT], bf[C::NTL];
+#pragma unroll
+            for (int t = 0; t < C::MT; ++t) af[t] = *(const i32x4 *)&As[cur][arow0 + t * 16 * C::ROW + kk];
+#pragma unroll
+            for (int t = 0; t < C::NTL; ++t) bf[t] = *(const i32x4 *)&Bs[cur][brow0 + t * 16 * C::ROW + kk];
+#pragma unroll
+            for (int tn = 0; tn < C::NTL; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < C::MT; ++tm) {
+                    if (I8) {
+                        iacc[tn][tm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[tn], af[tm], iacc[tn][tm], 0, 0, 0);
+                    } else {
+                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[tm]), acc[tn][tm], 0,
+                            0, 0);
+                    }
+                }
+        }
+    };
+    // Loads and stores in the loop are unconditional (the slice index is
+    // clamped, so the last iterations re-fetch the final slice into a buffer
+    // nobody reads again): a conditional load would make the compiler's
+    // counter merge at the join wait for every outstanding load.
+    const int last = (nk - 1) * KB;
+    if (C::PF == 1) {
+        // One register stage: slice kt+1 is fetched while slice kt is multiplied.
+        gload(0, 0);
+        sstore(0, 0);
+        lds_barrier();
+        for (int kt = 0; kt < nk; ++kt) {
+            gload(0, min((kt + 1) * KB, last));
+            __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+            compute(kt & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            sstore(0, (kt + 1) & 1);
+            lds_barrier();
+        }
+    } else {
+        // Two register stages; slice kt lives in LDS buffer kt%2 and, before
+        // that, in register stage kt%2.
+        auto step = [&](int kt, int par) {
+            gload(par, min((kt + 2) * KB, last));  // stage par was stored last iteration
+            __builtin_amdgcn_sched_barrier(0);     // keep the prefetch ahead of the MFMAs
+            compute(par);
+            __builtin_amdgcn_sched_barrier(0);
+            sstore(par ^ 1, par ^ 1);
+            lds_barrier();
+        };
+        gload(0, 0);
+        gload(1, min(KB, last));
+        sstore(0, 0);
+        lds_barrier();
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            step(kt, 0);
+            step(kt + 1, 1);
+        }
+        if (kt < nk) step(kt, 0);
+    }
+
+    static_assert((C::NT / 64) * 32 * (64 * 4 + 16) <= 2 * C::BM * C::ROW, "epilogue staging exceeds LDS");
+    if (KFULL && g.epi_lds)
+        store_tiles_lds<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0]);
+    else
+        store_tiles<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, acc, iacc);
+}
+
+// Variant for large M: only the weight tile goes through LDS.  Waves are
+// stacked along M, and each wave loads its activation fragments straight
+// from global memory into registers in the MFMA operand layout (lane reads
+// 16 bytes of row lane%16 at K offset (lane/16)·16), one slice ahead.  This
+// removes the activation tile's LDS write and read traffic, which otherwise
+// saturates the LDS pipe before the MFMA pipe.
+template <class C, bool I8, int ACT, bool OUT_F32>
+__global__ __launch_bounds__(C::NT) void gemm_adirect_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    int mt, nt;
+    tile_coords(mt, nt);
+    const int m0 = mt * C::BM, n0 = nt * C::BN;
+    constexpr int ESZ = I8 ? 1 : 2;
+    const int kbytes = g.K * ESZ;
+    const uint8_t *A = (const uint8_t *)g.A;
+    const uint8_t *B = (const uint8_t *)g.B;
+    const size_t lda = (size_t)g.lda * ESZ, ldb = (size_t)g.ldb * ESZ;
+
+    const uint8_t *arow[C::MT];
+#pragma unroll
+    for (int t = 0; t < C::MT; ++t) {
+        const int r = min(m0 + (wm * C::MT + t) * 16 + (lane & 15), g.M - 1);
+        arow[t] = A + (size_t)r * lda + (lane >> 4) * 16;
+    }
+    const uint8_t *bsrc[C::BCH];
+#pragma unroll
+    for (int i = 0; i < C::BCH; ++i) {
+        const int c = tid + i * C::NT;
+        bsrc[i] = B + (size_t)min(n0 + (c >> 3), g.N - 1) * ldb + (c & 7) * 16;
+    }
+
+    i32x4 af[2][C::MT][2];  // [stage][m tile][k step]
+    i32x4 rb[C::BCH];
+    auto aload = [&](int st, int kb0) {
+#pragma unroll
+        for (int t = 0; t < C::MT; ++t)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) af[st][t][ks] = *(const i32x4 *)(arow[t] + kb0 + ks * 64);
+    };
+    auto bload = [&](int kb0) {
+#pragma unroll
+        for (int i = 0; i < C::BCH; ++i) rb[i] = *(const i32x4 *)(bsrc[i] + kb0);
+    };
+    auto bstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < C::BCH; ++i) {
+            const int c = tid + i * C::NT;
+            *(i32x4 *)&Bs[buf][(c >> 3) * C::ROW + (c & 7) * 16] = rb[i];
+        }
+    };
+
+    f32x4 acc[C::NTL][C::MT];
+    i32x4 iacc[C::NTL][C::MT];
+    const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < C::NTL; ++a)
+#pragma unroll
+        for (int b = 0; b < C::MT; ++b) {
+            acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            iacc[a][b] = zero;
+        }
+
+    const int nk = kbytes / KB;  // launcher guarantees K·ESZ % 128 == 0
+    const int last = (nk - 1) * KB;
+    const int brow0 = (wn * C::NTL * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
+    auto compute = [&](int par) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            i32x4 bf[C::NTL];
+#pragma unroll
+            for (int t = 0; t < C::NTL; ++t) bf[t] = *(const i32x4 *)&Bs[par][brow0 + t * 16 * C::ROW + ks * 64];
+#pragma unroll
+            for (int tn = 0; tn < C::NTL; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < C::MT; ++tm) {
+                    if (I8) {
+                        iacc[tn][tm] =
+                            __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[tn], af[par][tm][ks], iacc[tn][tm], 0, 0, 0);
+                    } else {
+                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[par][tm][ks]),
+                            acc[tn][tm], 0, 0, 0);
+                    }
+                }
+        }
+    };
+    // Slice kt: activations in register stage kt%2, weights in LDS buffer
+    // kt%2.  Weight loads for kt+1 are issued before activation loads so the
+    // wait before the LDS store leaves the activation loads in flight.
+    auto step = [&](int kt, int par) {
+        const int nxt = min((kt + 1) * KB, last);
+        bload(nxt);
+        aload(par ^ 1, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(par);
+        __builtin_amdgcn_sched_barrier(0);
+        bstore(par ^ 1);
+        lds_barrier();
+    };
+    bload(0);
+    aload(0, 0);
+    bstore(0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        step(kt, 0);
+        step(kt + 1, 1);
+    }
+    if (kt < nk) step(kt, 0);
+
+    store_tiles<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, acc, iacc);
+}
+
+// Tile configurations (block tile, wave grid, row pad, prefetch depth).
+// 0–3 stage both operands through LDS; 4–6 stage only the weights.
+using C0 = Cfg<128, 128, 2, 2, 16, 1>;
+using C1 = Cfg<128, 128, 2, 2, 32, 1>;
+using C2 = Cfg<256, 128, 4, 2, 32, 1>;
+using C3 = Cfg<256, 128, 4, 2, 32, 2>;
+using C4 = Cfg<256, 128, 4, 2, 32, 1>;
+using C5 = Cfg<256, 256, 2, 4, 16, 1>;
+using C6 = Cfg<256, 256, 2, 4, 16, 2>;
+
+template <class C, bool I8, bool KFULL>
+hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
+    dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
+    dim3 block(C::NT);
+    if (act == fh::ACT_NONE && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_NONE, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_NONE) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_NONE, true>), grid, block, 0, s, g);
+    else if (act == fh::ACT_GELU && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_GELU, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_GELU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_GELU, true>), grid, block, 0, s, g);
+    else if (act == fh::ACT_SWIGLU && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_SWIGLU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, true>), grid, block, 0, s, g);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <class C, bool I8>
+hipError_t launch_adirect(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
+    dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
+    dim3 block(C::NT);
+    if (act == fh::ACT_NONE && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_NONE, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_NONE) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_NONE, true>), grid, block, 0, s, g);
+    else if (act == fh::ACT_GELU && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_GELU, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_GELU) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_GELU, true>), grid, block, 0, s, g);
+    else if (act == fh::ACT_SWIGLU && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_SWIGLU, false>), grid, block, 0, s, g);
+    else if (act == fh::ACT_SWIGLU) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_SWIGLU, true>), grid, block, 0, s, g);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// FUTON_GEMM_TILE=0..6 pins a configuration (tuning knob); otherwise the
+// choice depends only on the problem shape.
+int forced_cfg() {
+    static const int v = [] {
+        const char *e = getenv("FUTON_GEMM_TILE");
+        return e ? atoi(e) : -1;
+    }();
+    return v;
+}
+
+template <bool I8>
+hipError_t launch(const GemmArgs &ga, int act, bool out_f32, hipStream_t s) {
+    if (ga.M <= 0) return hipSuccess;
+    GemmArgs g = ga;
+    const int nout = act == fh::ACT_SWIGLU ? g.N / 2 : g.N;
+    g.epi_lds = (nout % (act == fh::ACT_SWIGLU ? 32 : 64) == 0) && (g.N % 64 == 0) &&
+                (out_f32 || (!g.resid && !g.resid_h)) && (g.ldc % 8 == 0) && (!g.resid && !g.resid_h || g.ldr % 4 == 0);
+    const bool kfull = (g.K * (I8 ? 1 : 2)) % KB == 0;
+    if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, s);
+    int cfg = forced_cfg();
+    if (cfg < 0 || cfg > 6) {
+        // Largest tile that still gives every CU at least one block.
+        const long m256 = (g.M + 255) / 256;
+        if (g.N % 256 == 0 && m256 * (g.N / 256) >= 256) cfg = 5;
+        else if (m256 * ((g.N + 127) / 128) >= 256) cfg = 3;
+        else cfg = 0;
+    }
+    switch (cfg) {
+    case 1: return launch_cfg<C1, I8, true>(g, act, out_f32, s);
+    case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, s);
+    case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, s);
+    case 4: return launch_adirect<C4, I8>(g, act, out_f32, s);
+    case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, s);
+    case 6: return launch_cfg<C6, I8, true>(g, act, out_f32, s);
+    default: return launch_cfg<C0, I8, true>(g, act, out_f32, s);
+    }
 }
 
 }  // namespace

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t *ids, const
         }
         v[j] = x;
     }
-    ln_row(v, H, gamma, beta, eps, x32 + row * H, x16 + row * H);
+    ln_row(v, H, gamma, beta, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
 }
 
 // x = LN(y) per row (y already holds proj + bias + residual) — model.go:596-599, 631-633.
@@ -89,14 +89,19 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *y, int M, 
         const int e = lane + 64 * j;
         v[j] = e < H ? src[e] : 0.f;
     }
-    ln_row(v, H, gamma, beta, eps, x32 + (size_t)row * H, x16 ? x16 + (size_t)row * H : nullptr);
+    ln_row(v, H, gamma, beta, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 ? x16 + (size_t)row * H : nullptr);
 }
 
-// xc[i] = x[offsets[i]]: the CLS rows the last layer computes (model.go:403-410).
-__global__ void gather_rows_kernel(const float *x32, const int32_t *offsets, int H, float *xc32) {
+// xc[i] = x[offsets[i]]: the CLS rows the last layer computes (model.go:403-410),
+// from the f32 and/or f16 stream.
+__global__ void gather_rows_kernel(const float *x32, const f16 *x16, const int32_t *offsets, int H, float *xc32,
+                                   f16 *xc16) {
     const int seq = blockIdx.x;
-    const float *src = x32 + (size_t)offsets[seq] * H;
-    for (int e = threadIdx.x; e < H; e += blockDim.x) xc32[(size_t)seq * H + e] = src[e];
+    const size_t src = (size_t)offsets[seq] * H, dst = (size_t)seq * H;
+    for (int e = threadIdx.x; e < H; e += blockDim.x) {
+        if (x32) xc32[dst + e] = x32[src + e];
+        if (x16) xc16[dst + e] = x16[src + e];
+    }
 }
 
 // Per-row absmax int8 quantization of activations — native/quant.go:42-70:
@@ -124,6 +129,81 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *x, int 
         dst[e] = (int8_t)c;
     }
     if (lane == 0) scale[row] = __fdiv_rn(amax, 127.0f);
+}
+
+// Width-specialized LayerNorm for H = 64·VPL: every lane owns VPL elements
+// (e = lane + 64·j), no bounds branches.  Statistics in float32, two-pass
+// (mean, then centered variance), which keeps the relative error of the
+// normalized values near 1e-7 for these widths.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int VPL>
+__device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float *gamma, const float *beta, float eps,
+                                         float *o32, f16 *o16) {
+    constexpr int H = 64 * VPL;
+    const int lane = threadIdx.x & 63;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) s += v[j];
+    const float mean = wave_sum_f32(s) * (1.0f / H);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const float d = v[j] - mean;
+        q += d * d;
+    }
+    const float var = wave_sum_f32(q) * (1.0f / H);
+    const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int e = lane + 64 * j;
+        const float y = (v[j] - mean) * inv * gamma[e] + beta[e];
+        if (o32) o32[e] = y;
+        o16[e] = (f16)y;
+    }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void layer_norm_v_kernel(const float *y, int M, const float *gamma,
+                                                           const float *beta, float eps, float *x32, f16 *x16) {
+    constexpr int H = 64 * VPL;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int lane = threadIdx.x & 63;
+    const float *src = y + (size_t)row * H;
+    float v[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) v[j] = src[lane + 64 * j];
+    ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 + (size_t)row * H);
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, const int32_t *offsets,
+                                                         const float *word, const float *type0, const float *pos,
+                                                         const float *gamma, const float *beta, float eps,
+                                                         float *x32, f16 *x16) {
+    constexpr int H = 64 * VPL;
+    const int seq = blockIdx.y;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= L) return;
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)(start + t);
+    const float *w = word + (size_t)ids[row] * H;
+    float v[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int e = lane + 64 * j;
+        float x = w[e];
+        if (type0) x += type0[e];
+        if (pos) x += pos[(size_t)t * H + e];
+        v[j] = x;
+    }
+    ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
 }
 
 __device__ double block_sum_f64(double v, double *red) {
@@ -199,21 +279,43 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
                     const float *word, const float *type0, const float *pos, const float *gamma,
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s) {
     if (nseq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(embed_ln_kernel, dim3((max_len + 3) / 4, nseq), dim3(256), 0, s, ids, offsets,
-                       word, type0, pos, gamma, beta, eps, H, x32, x16);
+    const dim3 grid((max_len + 3) / 4, nseq);
+#define FH_EMB_V(V)                                                                                          \
+    case V: hipLaunchKernelGGL(embed_ln_v_kernel<V>, grid, dim3(256), 0, s, ids, offsets, word, type0, pos, gamma, \
+                               beta, eps, x32, x16);                                                         \
+        return hipGetLastError();
+    if (H % 64 == 0) {
+        switch (H / 64) {
+            FH_EMB_V(4) FH_EMB_V(6) FH_EMB_V(8) FH_EMB_V(12) FH_EMB_V(16)
+        default: break;
+        }
+    }
+#undef FH_EMB_V
+    hipLaunchKernelGGL(embed_ln_kernel, grid, dim3(256), 0, s, ids, offsets, word, type0, pos, gamma, beta, eps, H,
+                       x32, x16);
     return hipGetLastError();
 }
 hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
                       float *x32, f16 *x16, hipStream_t s) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(layer_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, y, M, H, gamma, beta, eps,
-                       x32, x16);
+    const dim3 grid((M + 3) / 4);
+#define FH_LN_V(V)                                                                                          \
+    case V: hipLaunchKernelGGL(layer_norm_v_kernel<V>, grid, dim3(256), 0, s, y, M, gamma, beta, eps, x32, x16); \
+        return hipGetLastError();
+    if (H % 64 == 0 && gamma && x16) {
+        switch (H / 64) {
+            FH_LN_V(4) FH_LN_V(6) FH_LN_V(8) FH_LN_V(12) FH_LN_V(16)
+        default: break;
+        }
+    }
+#undef FH_LN_V
+    hipLaunchKernelGGL(layer_norm_kernel, grid, dim3(256), 0, s, y, M, H, gamma, beta, eps, x32, x16);
     return hipGetLastError();
 }
-hipError_t gather_rows(const float *x32, const int32_t *offsets, int nseq, int H, float *xc32,
-                       hipStream_t s) {
+hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,
+                       f16 *xc16, hipStream_t s) {
     if (nseq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq), dim3(128), 0, s, x32, offsets, H, xc32);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq), dim3(128), 0, s, x32, x16, offsets, H, xc32, xc16);
     return hipGetLastError();
 }
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
