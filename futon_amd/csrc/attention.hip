@@ -6,35 +6,49 @@
 // The reference runs each sequence unpadded; here sequences are packed
 // back to back (offsets[]) and every key outside the query's own sequence
 // is excluded, which is the same function.  RoPE (rotateHalf,
-// model.go:705-712) is applied to q and k as they are staged.
+// model.go:705-712) is applied to q (in registers) and k (in LDS).
 //
-// Block = (query block of 16·WAVES rows, head, sequence).  K and V of a
-// 64-key block are staged once per block in LDS (V transposed).  Each wave
-// computes Sᵀ = K·Qᵀ with v_mfma_f32_16x16x32_f16 so that a lane owns four
-// scores of ONE query (lane%16); the online-softmax statistics of a query
-// therefore live in the lanes that also own its output column, and P feeds
-// the Oᵀ = Vᵀ·Pᵀ MFMA straight from registers (the key order inside the
-// contraction is permuted identically on both operands).
+// Block = (query group, head, sequence); each wave owns QT tiles of 16
+// queries.  K and V of a KBLK-key block are staged once per block in LDS
+// (V transposed).  Each wave computes Sᵀ = K·Qᵀ with
+// v_mfma_f32_16x16x32_f16 so that a lane owns four scores of ONE query
+// (lane%16): the online-softmax statistics of a query live in the lanes
+// that also own its output column, and P feeds the Oᵀ = Vᵀ·Pᵀ MFMA straight
+// from registers (the key order inside the contraction is permuted
+// identically on both operands).  Q fragments are loaded from global memory
+// directly in the MFMA operand layout.
 #include "fh_common.h"
 
 namespace {
 
-constexpr int KBLK = 64;  // keys per staged block
-
-template <int D, int WAVES, bool OUT_F32, bool ROPE>
+template <int D, int WAVES, int QT, int KBLK, bool OUT_F32, bool ROPE>
 __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
-    constexpr int QROWS = 16 * WAVES;
-    constexpr int KS = D + 8;      // K / Q LDS row stride (halves)
-    constexpr int VS = KBLK + 8;   // Vᵀ LDS row stride (halves)
-    __shared__ __attribute__((aligned(16))) f16 Qs[QROWS * KS];
+    constexpr int QROWS = 16 * QT * WAVES;
+    constexpr int KS = D + 8;     // K LDS row stride (halves)
+    constexpr int VS = KBLK + 8;  // Vᵀ LDS row stride (halves)
+    constexpr int NKT = KBLK / 16;
     __shared__ __attribute__((aligned(16))) f16 Ks[KBLK * KS];
     __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
 
-    const int seq = blockIdx.z, head = blockIdx.y;
+    // Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
+    // contiguous range of (sequence, head, query group) in that order: all
+    // heads of a sequence then share one L2, which fetches the sequence's
+    // qkv rows once instead of once per XCD.
+    int seq, head, qg;
+    {
+        const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * gridDim.z;
+        const int pid = (blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
+        const int xcd = pid & 7, idx = pid >> 3, q8 = nb >> 3, r8 = nb & 7;
+        const int logical = xcd * q8 + min(xcd, r8) + idx;
+        qg = logical % gx;
+        const int t = logical / gx;
+        head = t % gy;
+        seq = t / gy;
+    }
     const int start = a.offsets[seq];
     const int L = a.offsets[seq + 1] - start;
     const int nq = min(L, a.q_limit);
-    const int q0 = blockIdx.x * QROWS;
+    const int q0 = qg * QROWS;
     if (q0 >= nq) return;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -43,40 +57,54 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
     const int chunks = d >> 3;  // 16-byte chunks per row (d % 8 == 0)
     const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
 
-    // ── stage Q (rows clamped into the sequence; padding dims zero) ──
-    for (int c = tid; c < QROWS * (D / 8); c += WAVES * 64) {
-        const int r = c / (D / 8), ch = c % (D / 8);
-        const int q = min(q0 + r, L - 1);
-        f16x8 v = z8;
-        if (ch < chunks) v = *(const f16x8 *)(a.qkv + (size_t)(start + q) * ld + head * d + ch * 8);
-        *(f16x8 *)&Qs[r * KS + ch * 8] = v;
-    }
-    __syncthreads();
-    if (ROPE) {
-        for (int c = tid; c < QROWS * half; c += WAVES * 64) {
-            const int r = c / half, i = c % half;
-            const int pos = min(q0 + r, L - 1);
-            const float cs = a.rope_cos[pos * half + i], sn = a.rope_sin[pos * half + i];
-            const float x1 = (float)Qs[r * KS + i], x2 = (float)Qs[r * KS + i + half];
-            Qs[r * KS + i] = (f16)(x1 * cs - x2 * sn);
-            Qs[r * KS + i + half] = (f16)(x2 * cs + x1 * sn);
+    // ── Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds dims
+    //    [dk·32 + (lane/16)·8, +8) of query lane%16 of each tile. ──
+    f16x8 qf[QT][D / 32];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int q = min(q0 + (wave * QT + qt) * 16 + (lane & 15), L - 1);
+        const f16 *qrow = a.qkv + (size_t)(start + q) * ld + head * d;
+#pragma unroll
+        for (int dk = 0; dk < D / 32; ++dk) {
+            const int j0 = dk * 32 + (lane >> 4) * 8;
+            f16x8 v = z8;
+            if (j0 < d) v = *(const f16x8 *)(qrow + j0);
+            if (ROPE && j0 < d) {
+                // Partner dims j ± half: inside this chunk when half < 8 (d = 8),
+                // else the aligned chunk half away.
+                f16x8 p = v;
+                if (half >= 8) p = *(const f16x8 *)(qrow + (j0 < half ? j0 + half : j0 - half));
+                f16x8 r;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = j0 + e;
+                    const int i = j < half ? j : j - half;  // table index
+                    const float cs = a.rope_cos[q * half + i], sn = a.rope_sin[q * half + i];
+                    float partner;
+                    if (half >= 8) partner = (float)p[e];
+                    else partner = (float)v[(e + half) & 7];
+                    const float x = (float)v[e];
+                    r[e] = (f16)(j < half ? x * cs - partner * sn : x * cs + partner * sn);
+                }
+                v = r;
+            }
+            qf[qt][dk] = v;
         }
-        __syncthreads();
     }
-    // B operand of Sᵀ = K·Qᵀ: lane holds dims [dk·32 + (lane/16)·8, +8) of query lane%16.
-    f16x8 qf[D / 32];
-#pragma unroll
-    for (int dk = 0; dk < D / 32; ++dk)
-        qf[dk] = *(const f16x8 *)&Qs[(wave * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
 
-    f32x4 o[D / 16];
+    f32x4 o[QT][D / 16];
+    float m_run[QT], l_run[QT];
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    for (int qt = 0; qt < QT; ++qt) {
+        m_run[qt] = -INFINITY;
+        l_run[qt] = 0.f;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) o[qt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
     const float sl2 = a.scale_log2e;
 
     for (int kb0 = 0; kb0 < L; kb0 += KBLK) {
-        __syncthreads();  // previous block's K/V fully consumed
+        if (kb0 > 0) __syncthreads();  // previous block's K/V fully consumed
         for (int c = tid; c < KBLK * (D / 8); c += WAVES * 64) {
             const int r = c / (D / 8), ch = c % (D / 8);
             const int key = min(kb0 + r, L - 1);
@@ -102,105 +130,116 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
             }
             __syncthreads();
         }
+        const int kvalid = L - kb0;                   // valid keys from kb0 on
+        const int nkt = min(NKT, (kvalid + 15) >> 4);  // key tiles holding valid keys
 
-        // Sᵀ tiles: s[kt][i] = score(key kb0 + kt·16 + (lane/16)·4 + i, query lane%16).
-        f32x4 s[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int qt = 0; qt < QT; ++qt) {
+            if (q0 + (wave * QT + qt) * 16 >= nq) continue;  // tile holds no live query (wave-uniform)
+            // Sᵀ tiles: s[kt][i] = score(key kb0 + kt·16 + (lane/16)·4 + i, query lane%16).
+            f32x4 s[NKT];
+            float mx = -INFINITY;
 #pragma unroll
-            for (int dk = 0; dk < D / 32; ++dk) {
-                const f16x8 kf =
-                    *(const f16x8 *)&Ks[(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[dk], s[kt], 0, 0, 0);
+            for (int kt = 0; kt < NKT; ++kt) {
+                if (kt >= nkt) continue;
+                s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int dk = 0; dk < D / 32; ++dk) {
+                    const f16x8 kf = *(const f16x8 *)&Ks[(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qt][dk], s[kt], 0, 0, 0);
+                }
+                if (kt * 16 + 16 > kvalid) {  // boundary tile: mask keys past the sequence
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (kt * 16 + (lane >> 4) * 4 + i >= kvalid) s[kt][i] = -INFINITY;
+                }
+                mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
             }
-        }
-        float mx = -INFINITY;
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
+            const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+            float psum = 0.f;
+            f16x8 pf[NKT / 2];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb0 + kt * 16 + (lane >> 4) * 4 + i;
-                if (key >= L) s[kt][i] = -INFINITY;
-                mx = fmaxf(mx, s[kt][i]);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx * sl2);  // log2-scaled running max
-        const float corr = exp2f(m_run - m_new);
-        float psum = 0.f;
-        f16x8 pf[2];
+                for (int i = 0; i < 4; ++i) {
+                    const float p = kt < nkt ? __builtin_amdgcn_exp2f(s[kt][i] * sl2 - m_new) : 0.f;
+                    psum += p;
+                    pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
+                }
+            psum += __shfl_xor(psum, 16, 64);
+            psum += __shfl_xor(psum, 32, 64);
+            l_run[qt] = l_run[qt] * corr + psum;
+            m_run[qt] = m_new;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = exp2f(s[kt][i] * sl2 - m_new);
-                psum += p;
-                pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
-            }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < D / 16; ++t) o[t] *= corr;
+            for (int t = 0; t < D / 16; ++t) o[qt][t] *= corr;
 
-        // Oᵀ += Vᵀ·Pᵀ over two 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
+            // Oᵀ += Vᵀ·Pᵀ over 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
+            for (int c = 0; c < NKT / 2; ++c) {
+                if (2 * c >= nkt) continue;
 #pragma unroll
-            for (int t = 0; t < D / 16; ++t) {
-                const f16 *vrow = &Vt[(t * 16 + (lane & 15)) * VS + c * 32 + (lane >> 4) * 4];
-                const f16x4 lo = *(const f16x4 *)vrow;
-                const f16x4 hi = *(const f16x4 *)(vrow + 16);
-                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[t], 0, 0, 0);
+                for (int t = 0; t < D / 16; ++t) {
+                    const f16 *vrow = &Vt[(t * 16 + (lane & 15)) * VS + c * 32 + (lane >> 4) * 4];
+                    const f16x4 lo = *(const f16x4 *)vrow;
+                    const f16x4 hi = *(const f16x4 *)(vrow + 16);
+                    const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[qt][t], 0, 0, 0);
+                }
             }
         }
     }
 
-    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4].
-    const int q = q0 + wave * 16 + (lane & 15);
-    if (q >= nq) return;
-    const float inv = 1.0f / l_run;
-    const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
+    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4] of each tile.
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-        const int dim = t * 16 + (lane >> 4) * 4;
-        if (dim >= d) continue;
-        const f32x4 v = o[t] * inv;
-        if (OUT_F32) {
-            *(f32x4 *)((float *)a.out + orow * a.ldo + head * d + dim) = v;
-        } else {
-            const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-            *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * d + dim) = h;
+    for (int qt = 0; qt < QT; ++qt) {
+        const int q = q0 + (wave * QT + qt) * 16 + (lane & 15);
+        if (q >= nq) continue;
+        const float inv = 1.0f / l_run[qt];
+        const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+            const int dim = t * 16 + (lane >> 4) * 4;
+            if (dim >= d) continue;
+            const f32x4 v = o[qt][t] * inv;
+            if (OUT_F32) {
+                *(f32x4 *)((float *)a.out + orow * a.ldo + head * d + dim) = v;
+            } else {
+                const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * d + dim) = h;
+            }
         }
     }
 }
 
-template <int D, int WAVES>
-hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope,
-                    hipStream_t s) {
-    constexpr int QROWS = 16 * WAVES;
+template <int D, int WAVES, int QT, int KBLK>
+hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
+    constexpr int QROWS = 16 * QT * WAVES;
     const int qmax = min(max_len, a.q_limit);
     dim3 grid((qmax + QROWS - 1) / QROWS, a.H / a.d, nseq);
     dim3 block(WAVES * 64);
     if (out_f32) {
-        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<D, WAVES, true, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, false>), grid, block, 0, s, a);
     } else {
-        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<D, WAVES, false, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, false>), grid, block, 0, s, a);
     }
     return hipGetLastError();
 }
 
 template <int D>
-hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope,
-                    hipStream_t s) {
-    // One wave per (sequence, head) when only the CLS row is queried.
-    if (a.q_limit <= 16) return launch_d<D, 1>(a, nseq, max_len, out_f32, rope, s);
-    return launch_d<D, 4>(a, nseq, max_len, out_f32, rope, s);
+hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
+    // CLS row only: one wave per (sequence, head).
+    if (a.q_limit <= 16) {
+        if (max_len <= 128) return launch_d<D, 1, 1, 128>(a, nseq, max_len, out_f32, rope, s);
+        return launch_d<D, 1, 1, 64>(a, nseq, max_len, out_f32, rope, s);
+    }
+    // Short sequences: one block covers every query and stages K/V once.
+    if (max_len <= 128) return launch_d<D, 4, 2, 128>(a, nseq, max_len, out_f32, rope, s);
+    return launch_d<D, 4, 1, 64>(a, nseq, max_len, out_f32, rope, s);
 }
 
 }  // namespace

@@ -522,8 +522,8 @@ using C1 = Cfg<128, 128, 2, 2, 32, 1>;
 using C2 = Cfg<256, 128, 4, 2, 32, 1>;
 using C3 = Cfg<256, 128, 4, 2, 32, 2>;
 using C4 = Cfg<256, 128, 4, 2, 32, 1>;
-using C5 = Cfg<256, 256, 2, 4, 16, 1>;
-using C6 = Cfg<256, 256, 2, 4, 16, 2>;
+using C5 = Cfg<256, 256, 2, 4, 32, 1>;
+using C6 = Cfg<256, 128, 4, 2, 32, 1>;
 
 template <class C, bool I8, bool KFULL>
 hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
