@@ -41,7 +41,42 @@ def parse():
     ap.add_argument("--pack-root", default=os.path.join(tempfile.gettempdir(), "futon_bench_packs"))
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 launches) and exit; its "
+                         "FETCH_SIZE/WRITE_SIZE counters calibrate the per-launch traffic figures")
     return ap.parse_args()
+
+
+def copy_probe(mib: int) -> None:
+    """A plain f32 device-to-device copy of known size, for counter calibration."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
+
+
+def load_traffic(kernel_class: str, workload: str):
+    """HBM bytes per launch of `kernel_class` from the committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs, each divided by what the same
+    counter reads per byte of a plain copy), or None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_class}_{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            k, sep, v = line.partition(":")
+            if sep and k.strip() in ("fetch_kib_per_dispatch", "write_kib_per_dispatch", "copy_fetch_factor",
+                                     "copy_write_factor"):
+                vals[k.strip()] = float(v.split()[0])
+    if len(vals) != 4:
+        return None
+    return (vals["fetch_kib_per_dispatch"] / vals["copy_fetch_factor"] +
+            vals["write_kib_per_dispatch"] / vals["copy_write_factor"]) * 1024.0
 
 
 def flops_per_embedding(cfg: dict, L: int) -> float:
@@ -84,6 +119,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are out of scope",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
     import torch
     from futon_amd import native, synth
 
@@ -129,17 +167,20 @@ def main():
     dom = max(prof, key=lambda k: prof[k]["ms"])
     pd = prof[dom]
     per_launch_ms = pd["ms"] / max(pd["launches"], 1)
+    traffic = load_traffic(dom, w.name)
     if pd["flops"] > 0:
         peak = PEAK_I8_TOPS if w.q8 and dom.startswith("gemm") else PEAK_F16_TFLOPS
         achieved = pd["flops"] / pd["launches"] / (per_launch_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": None,
-                "per_launch_flops": pd["flops"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3)}
+                "frac": round(achieved / peak, 4), "traffic": traffic,
+                "per_launch_flops": pd["flops"] / pd["launches"], "per_launch_bytes": pd["bytes"] / pd["launches"],
+                "per_launch_us": round(per_launch_ms * 1e3, 3), "launches_per_step": pd["launches"] // args.steps}
     else:
         achieved = pd["bytes"] / pd["launches"] / (per_launch_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "per_launch_bytes": pd["bytes"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3)}
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "per_launch_bytes": pd["bytes"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3),
+                "launches_per_step": pd["launches"] // args.steps}
     gemm_ms = sum(prof[k]["ms"] for k in GEMM_CLASSES)
     gemm_fl = sum(prof[k]["flops"] for k in GEMM_CLASSES)
     gemm_tf = gemm_fl / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0

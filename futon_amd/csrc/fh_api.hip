@@ -126,11 +126,12 @@ struct DevLayer {
 
 enum KClass {
     K_EMBED, K_GEMM_QKV, K_ATTN, K_GEMM_OUT, K_LN, K_GEMM_FFN1, K_GEMM_FC2, K_QUANT, K_GATHER, K_POOL,
+    K_CLS_TAIL,  // last CLS layer after its QKV GEMM: attention for row 0 and every M = nseq launch
     K_NCLASS
 };
 const char *kClassNames[K_NCLASS] = {"embed_ln",  "gemm_qkv", "attention", "gemm_out",
                                      "layer_norm", "gemm_ffn1", "gemm_fc2", "quantize_rows",
-                                     "gather_cls", "pool_l2"};
+                                     "gather_cls", "pool_l2",    "cls_last_layer"};
 
 struct ProfPending {
     int cls;
@@ -455,16 +456,16 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     return FH_OK;
 }
 
-int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s) {
-    Scope sc(m, K_QUANT, 0.0, (double)M * K * 5, s);
+int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s, int cls = K_QUANT) {
+    Scope sc(m, cls, 0.0, (double)M * K * 5, s);
     LCHK(fh::quantize_rows(x, M, K, ldx, m->xq, m->xs, s));
     return FH_OK;
 }
 
-int layer_norm(fh_model *m, const float *y, int M, const float *gw, const float *gb, float *x32, f16 *x16,
+int layer_norm(fh_model *m, int cls, const float *y, int M, const float *gw, const float *gb, float *x32, f16 *x16,
                hipStream_t s) {
     const int H = m->cfg.hidden_size;
-    Scope sc(m, K_LN, 0.0, (double)M * H * (4 + (x32 ? 4 : 0) + 2), s);
+    Scope sc(m, cls, 0.0, (double)M * H * (4 + (x32 ? 4 : 0) + 2), s);
     LCHK(fh::layer_norm(y, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
     return FH_OK;
 }
@@ -517,7 +518,7 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         a.scale_log2e = (float)(1.0 / std::sqrt((double)m->hd)) * 1.4426950408889634f;
         {
             const double nq_l = last_cls ? (double)T : b.sum_l2;  // Σ nq·L
-            Scope sc(m, K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * (q8 ? 4 : 2),
+            Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * (q8 ? 4 : 2),
                      s);
             LCHK(fh::attention(a, S, b.max_len, q8, s));
         }
@@ -527,46 +528,49 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         f16 *xo16 = last_cls ? m->xc16 : m->x16;
         const void *attn_in = last_cls ? m->attnc : m->attn;
         if (last_cls) {
-            Scope sc(m, K_GATHER, 0.0, (double)S * H * (f32res ? 8 : 4), s);
+            Scope sc(m, K_CLS_TAIL, 0.0, (double)S * H * (f32res ? 8 : 4), s);
             LCHK(fh::gather_rows(f32res ? m->x32 : nullptr, f32res ? nullptr : m->x16, b.d_offsets, S, H,
                                  f32res ? m->xc32 : nullptr, f32res ? nullptr : m->xc16, s));
         }
+        const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kLn = last_cls ? K_CLS_TAIL : K_LN;
+        const int kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1, kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
+        const int kQuant = last_cls ? K_CLS_TAIL : K_QUANT;
         const float *r32 = f32res ? xo32 : nullptr;
         const f16 *r16 = f32res ? nullptr : xo16;
 
         // out projection + bias + residual, norm1 (model.go:596-599)
         if (q8) {
-            if ((rc = quant(m, (const float *)attn_in, M, H, H, s))) return rc;
-            rc = gemm(m, K_GEMM_OUT, L.out, m->xq, H, m->xs, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
+            if ((rc = quant(m, (const float *)attn_in, M, H, H, s, kQuant))) return rc;
+            rc = gemm(m, kOut, L.out, m->xq, H, m->xs, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         } else {
-            rc = gemm(m, K_GEMM_OUT, L.out, attn_in, H, nullptr, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
+            rc = gemm(m, kOut, L.out, attn_in, H, nullptr, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, m->y32, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
+        if ((rc = layer_norm(m, kLn, m->y32, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
 
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // FFN (model.go:607-633)
         const int act = swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU;
         if (q8) {
-            if ((rc = quant(m, xo32, M, H, H, s))) return rc;
-            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
+            if ((rc = quant(m, xo32, M, H, H, s, kQuant))) return rc;
+            if ((rc = gemm(m, kFfn1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
                            act, true, s)))
                 return rc;
-            if ((rc = quant(m, (const float *)m->hbuf, M, I, I, s))) return rc;
-            rc = gemm(m, K_GEMM_FC2, L.fc2, m->xq, I, m->xs, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE, true,
+            if ((rc = quant(m, (const float *)m->hbuf, M, I, I, s, kQuant))) return rc;
+            rc = gemm(m, kFc2, L.fc2, m->xq, I, m->xs, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE, true,
                       s);
         } else {
-            if ((rc = gemm(m, K_GEMM_FFN1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
+            if ((rc = gemm(m, kFfn1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
                            act, false, s)))
                 return rc;
-            rc = gemm(m, K_GEMM_FC2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
+            rc = gemm(m, kFc2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, m->y32, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
+        if ((rc = layer_norm(m, kLn, m->y32, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
     }
 
     // pooling → Matryoshka → L2 (model.go:417-453)
