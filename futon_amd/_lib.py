@@ -87,9 +87,9 @@ def load():
     L.fh_last_error.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
     L.fh_model_device_bytes.restype = ctypes.c_int64
     L.fh_model_device_bytes.argtypes = [vp]
-    L.fh_op_gemm.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    L.fh_op_gemm.argtypes = [i32, vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, vp]
     L.fh_op_attention.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, i32, i32, vp]
-    L.fh_op_layer_norm.argtypes = [vp, i32, i32, vp, vp, ctypes.c_float, vp, vp, vp]
+    L.fh_op_layer_norm.argtypes = [vp, i32, i32, i32, vp, vp, ctypes.c_float, vp, vp, vp]
     L.fh_op_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
     L.fh_op_embed_ln.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, ctypes.c_float, i32, vp, vp, vp]
     L.fh_op_pool.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]

@@ -462,11 +462,11 @@ int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s, int
     return FH_OK;
 }
 
-int layer_norm(fh_model *m, int cls, const float *y, int M, const float *gw, const float *gb, float *x32, f16 *x16,
-               hipStream_t s) {
+int layer_norm(fh_model *m, int cls, const float *y32, const f16 *y16, int M, const float *gw, const float *gb,
+               float *x32, f16 *x16, hipStream_t s) {
     const int H = m->cfg.hidden_size;
-    Scope sc(m, cls, 0.0, (double)M * H * (4 + (x32 ? 4 : 0) + 2), s);
-    LCHK(fh::layer_norm(y, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
+    Scope sc(m, cls, 0.0, (double)M * H * ((y16 ? 2 : 4) + (x32 ? 4 : 0) + 2), s);
+    LCHK(fh::layer_norm(y32, y16, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
     return FH_OK;
 }
 
@@ -475,11 +475,13 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
     const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
     const bool q8 = c.q8 != 0, cls = c.pooling == FH_POOL_CLS, swiglu = c.activation == FH_ACT_SWIGLU;
     const float eps = (float)c.layer_norm_eps;
-    // Residual stream: binary16 between layers (the GEMM epilogues add it in
-    // f32), except on the Q8 path, whose activation quantizer reads the f32
-    // stream like quant.go:104-110.  The last layer's LN always writes f32
-    // for pooling.
+    // Residual stream: binary16 between layers, except on the Q8 path, whose
+    // activation quantizer reads the f32 stream like quant.go:104-110.  On
+    // the binary16 path the projection GEMMs add bias and residual in f32 and
+    // round once to binary16 (y16, aliasing y32's storage) for the LN; the
+    // last layer's LN always writes f32 for pooling.
     const bool f32res = q8;
+    f16 *const y16 = (f16 *)m->y32;
     int cp = 0, rc;
 
     {
@@ -544,11 +546,11 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
             rc = gemm(m, kOut, L.out, m->xq, H, m->xs, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
                       true, s);
         } else {
-            rc = gemm(m, kOut, L.out, attn_in, H, nullptr, M, L.out_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
-                      true, s);
+            rc = gemm(m, kOut, L.out, attn_in, H, nullptr, M, L.out_b, r32, r16, H, y16, H, fh::ACT_NONE,
+                      false, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, kLn, m->y32, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
+        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
 
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
@@ -566,11 +568,11 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
             if ((rc = gemm(m, kFfn1, L.ffn1, xo16, H, nullptr, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
                            act, false, s)))
                 return rc;
-            rc = gemm(m, kFc2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, r32, r16, H, m->y32, H, fh::ACT_NONE,
-                      true, s);
+            rc = gemm(m, kFc2, L.fc2, m->hbuf, I, nullptr, M, L.fc2_b, r32, r16, H, y16, H, fh::ACT_NONE,
+                      false, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, kLn, m->y32, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
+        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
     }
 
     // pooling → Matryoshka → L2 (model.go:417-453)

@@ -8,6 +8,7 @@ typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -52,15 +53,18 @@ struct AttnArgs {
 
 // Host-side launchers (defined next to their kernels).
 namespace fh {
-enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2 };
+// ACT_RES16 is internal to the GEMM launcher: no activation, binary16 output
+// with a binary16 residual added in f32 before the single rounding.
+enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_RES16 = 3 };
 hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s);
-hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
-                      float *x32, f16 *x16, hipStream_t s);
+// y32 or y16 (exactly one non-null) holds proj + bias + residual.
+hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
+                      float eps, float *x32, f16 *x16, hipStream_t s);
 hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,
                        f16 *xc16, hipStream_t s);
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,

@@ -13,17 +13,19 @@ namespace {
 int code_of(hipError_t e) { return e == hipSuccess ? FH_OK : FH_EHIP; }
 }  // namespace
 
-extern "C" int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const float *resid,
-                          const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N, int32_t K,
-                          int32_t act, int32_t out_f32, void *stream) {
+extern "C" int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const void *resid,
+                          int32_t resid_f16, const float *a_scale, const float *b_scale, void *C, int32_t M,
+                          int32_t N, int32_t K, int32_t act, int32_t out_f32, void *stream) {
     if (!A || !B || !C || M < 0 || N <= 0 || K <= 0) return FH_EINVAL;
+    if (resid && resid_f16 && (out_f32 || act != FH_OP_ACT_NONE || dtype != FH_OP_F16)) return FH_EINVAL;
     if (N % 4 || (act == FH_OP_ACT_SWIGLU && N % 32) || act < 0 || act > 2) return FH_EINVAL;
     if (dtype == FH_OP_I8 ? (K % 16 || !a_scale || !b_scale) : (dtype != FH_OP_F16 || K % 8)) return FH_EINVAL;
     GemmArgs g{};
     g.A = A;
     g.B = B;
     g.bias = bias;
-    g.resid = resid;
+    g.resid = resid_f16 ? nullptr : (const float *)resid;
+    g.resid_h = resid_f16 ? (const f16 *)resid : nullptr;
     g.a_scale = a_scale;
     g.b_scale = b_scale;
     g.C = C;
@@ -59,10 +61,11 @@ extern "C" int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t 
     return code_of(fh::attention(a, nseq, max_len, out_f32 != 0, (hipStream_t)stream));
 }
 
-extern "C" int fh_op_layer_norm(const float *y, int32_t M, int32_t H, const float *gamma, const float *beta, float eps,
-                                float *x32, void *x16, void *stream) {
+extern "C" int fh_op_layer_norm(const void *y, int32_t y_f16, int32_t M, int32_t H, const float *gamma,
+                                const float *beta, float eps, float *x32, void *x16, void *stream) {
     if (!y || !x32 || H <= 0 || H > 1024 || (gamma && !beta)) return FH_EINVAL;
-    return code_of(fh::layer_norm(y, M, H, gamma, beta, eps, x32, (f16 *)x16, (hipStream_t)stream));
+    return code_of(fh::layer_norm(y_f16 ? nullptr : (const float *)y, y_f16 ? (const f16 *)y : nullptr, M, H, gamma,
+                                  beta, eps, x32, (f16 *)x16, (hipStream_t)stream));
 }
 
 extern "C" int fh_op_quantize_rows(const float *x, int32_t M, int32_t K, int8_t *q, float *scale, void *stream) {

@@ -43,20 +43,18 @@ struct Cfg {
 // erfc fit the reference uses (native/mathf32.go:73-107; fractional error
 // < 1.2e-7), with the hardware exp.
 __device__ __forceinline__ float gelu_erf(float x) {
-    const float a = fabsf(x) * 0.70710678118654752f;
-    const float t = __builtin_amdgcn_rcpf(1.0f + 0.5f * a);
-    float p = 0.17087277f;
-    p = p * t - 0.82215223f;
-    p = p * t + 1.48851587f;
-    p = p * t - 1.13520398f;
-    p = p * t + 0.27886807f;
-    p = p * t - 0.18628806f;
-    p = p * t + 0.09678418f;
-    p = p * t + 0.37409196f;
-    p = p * t + 1.00002368f;
-    p = p * t - 1.26551223f;
-    const float c = t * __expf(p - a * a);  // erfc(|x|/√2)
-    return x < 0.f ? 0.5f * x * c : 0.5f * x * (2.0f - c);
+    // x·Φ(x) with erfc(z) = t·P(t)·exp(−z²), t = 1/(1 + p·z), z = |x|/√2
+    // (Abramowitz & Stegun 7.1.26, |error| ≤ 1.5e-7).  Constants folded:
+    // p/√2, ½·a_i, and exp(−x²/2) = 2^(−x²·½·log2 e).
+    const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.23164190f, 1.0f));
+    float q = 0.53070271f;
+    q = fmaf(q, t, -0.72657601f);
+    q = fmaf(q, t, 0.71070687f);
+    q = fmaf(q, t, -0.14224837f);
+    q = fmaf(q, t, 0.12741480f);
+    const float e = __builtin_amdgcn_exp2f((x * x) * -0.72134752f);
+    const float h = x * (q * t) * e;  // ½·x·erfc(|x|/√2)
+    return x < 0.f ? h : x - h;
 }
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -169,7 +167,8 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                                                 const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds) {
     static_assert(C::NTL * 16 == 64 && C::MT % 2 == 0, "staged epilogue expects 64-column wave tiles");
     constexpr int OC = ACT == fh::ACT_SWIGLU ? 32 : 64;  // output columns per wave
-    constexpr int ESZ = OUT_F32 ? 4 : 2;
+    constexpr bool R16 = ACT == fh::ACT_RES16;
+    constexpr int ESZ = (OUT_F32 || R16) ? 4 : 2;        // staged element size (bytes)
     constexpr int RS = OC * ESZ + 16;                    // LDS row stride (bytes)
     constexpr int CPR = OC * ESZ / 16;                   // 16-byte chunks per row
     uint8_t *region = lds + wave * 32 * RS;
@@ -217,12 +216,35 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 }
                 const int lc = (ACT == fh::ACT_SWIGLU ? (tn >> 1) : tn) * 16 + (lane >> 4) * 4;
                 uint8_t *dst = region + (h * 16 + (lane & 15)) * RS + lc * ESZ;
-                if (OUT_F32) {
+                if (OUT_F32 || R16) {
                     *(f32x4 *)dst = v;
                 } else {
                     *(f16x4 *)dst = (f16x4){(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
                 }
             }
+        }
+        if (R16) {
+            // 8 output columns per lane step: two staged f32 chunks plus the
+            // binary16 residual, rounded once, one 16-byte store.
+#pragma unroll
+            for (int j = 0; j < 32 * 8 / 64; ++j) {
+                const int c = lane + 64 * j, r = c >> 3, ch = c & 7;
+                const int grow = m0 + (wm * C::MT + 2 * p) * 16 + r;
+                const f32x4 lo = *(const f32x4 *)(region + r * RS + ch * 32);
+                const f32x4 hi = *(const f32x4 *)(region + r * RS + ch * 32 + 16);
+                if (grow >= g.M) continue;
+                const int gcol = ocol0 + ch * 8;
+                f16x8 rr = {};
+                if (g.resid_h) rr = *(const f16x8 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                f16x8 o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o[i] = (f16)(lo[i] + (float)rr[i]);
+                    o[4 + i] = (f16)(hi[i] + (float)rr[4 + i]);
+                }
+                *(f16x8 *)((f16 *)g.C + (size_t)grow * g.ldc + gcol) = o;
+            }
+            continue;
         }
         // Same-wave LDS accesses complete in order: the rows are readable now.
 #pragma unroll
@@ -535,6 +557,7 @@ hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
     else if (act == fh::ACT_GELU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_GELU, true>), grid, block, 0, s, g);
     else if (act == fh::ACT_SWIGLU && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, false>), grid, block, 0, s, g);
     else if (act == fh::ACT_SWIGLU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, true>), grid, block, 0, s, g);
+    else if (act == fh::ACT_RES16 && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_RES16, false>), grid, block, 0, s, g);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
@@ -567,17 +590,20 @@ template <bool I8>
 hipError_t launch(const GemmArgs &ga, int act, bool out_f32, hipStream_t s) {
     if (ga.M <= 0) return hipSuccess;
     GemmArgs g = ga;
+    if (act == fh::ACT_NONE && !out_f32 && g.resid_h && !g.resid) act = fh::ACT_RES16;
     const int nout = act == fh::ACT_SWIGLU ? g.N / 2 : g.N;
+    const bool has_res = g.resid || g.resid_h;
     g.epi_lds = (nout % (act == fh::ACT_SWIGLU ? 32 : 64) == 0) && (g.N % 64 == 0) &&
-                (out_f32 || (!g.resid && !g.resid_h)) && (g.ldc % 8 == 0) && (!g.resid && !g.resid_h || g.ldr % 4 == 0);
+                (out_f32 || act == fh::ACT_RES16 || !has_res) && (g.ldc % 8 == 0) && (!has_res || g.ldr % 8 == 0);
     const bool kfull = (g.K * (I8 ? 1 : 2)) % KB == 0;
     if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, s);
     int cfg = forced_cfg();
     if (cfg < 0 || cfg > 6) {
-        // Largest tile that still gives every CU at least one block.
+        // 256×256 when it still gives every CU a block; 256×128 down to half
+        // the CUs (it beats 128×128 on the N = H projections even there).
         const long m256 = (g.M + 255) / 256;
         if (g.N % 256 == 0 && m256 * (g.N / 256) >= 256) cfg = 5;
-        else if (m256 * ((g.N + 127) / 128) >= 256) cfg = 3;
+        else if (m256 * ((g.N + 127) / 128) >= 128) cfg = 3;
         else cfg = 0;
     }
     switch (cfg) {

@@ -76,18 +76,19 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int32_t *ids, const
 }
 
 // x = LN(y) per row (y already holds proj + bias + residual) — model.go:596-599, 631-633.
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float *y, int M, int H,
+template <class T>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const T *y, int M, int H,
                                                          const float *gamma, const float *beta,
                                                          float eps, float *x32, f16 *x16) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const int lane = threadIdx.x & 63;
-    const float *src = y + (size_t)row * H;
+    const T *src = y + (size_t)row * H;
     float v[MAXV];
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < H ? src[e] : 0.f;
+        v[j] = e < H ? (float)src[e] : 0.f;
     }
     ln_row(v, H, gamma, beta, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 ? x16 + (size_t)row * H : nullptr);
 }
@@ -131,14 +132,63 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *x, int 
     if (lane == 0) scale[row] = __fdiv_rn(amax, 127.0f);
 }
 
-// Width-specialized LayerNorm for H = 64·VPL: every lane owns VPL elements
-// (e = lane + 64·j), no bounds branches.  Statistics in float32, two-pass
-// (mean, then centered variance), which keeps the relative error of the
-// normalized values near 1e-7 for these widths.
+// Width-specialized LayerNorm for H = 64·VPL (VPL even).  A lane owns VPL
+// elements of its row: the first 256·(VPL/4) in 4-element chunks
+// (elements 4·(64·c + lane) .. +3 of chunk c), then, when VPL % 4 == 2, the
+// next 128 in pairs (256·(VPL/4) + 2·lane .. +1), so every access is a
+// 16/8-byte (f32) or 8/4-byte (f16) vector and a wave covers contiguous
+// memory.  Statistics in float32, two-pass (mean, then centered variance),
+// which keeps the relative error of the normalized values near 1e-7.
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+template <int VPL>
+__device__ __forceinline__ void ld_row(const float *p, int lane, float (&v)[VPL]) {
+    constexpr int N4 = VPL / 4;
+#pragma unroll
+    for (int c = 0; c < N4; ++c) {
+        const f32x4 t = *(const f32x4 *)(p + 4 * (64 * c + lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * c + i] = t[i];
+    }
+    if (VPL % 4) {
+        const f32x2 t = *(const f32x2 *)(p + 256 * N4 + 2 * lane);
+        v[4 * N4] = t[0];
+        v[4 * N4 + 1] = t[1];
+    }
+}
+template <int VPL>
+__device__ __forceinline__ void ld_row(const f16 *p, int lane, float (&v)[VPL]) {
+    constexpr int N4 = VPL / 4;
+#pragma unroll
+    for (int c = 0; c < N4; ++c) {
+        const f16x4 t = *(const f16x4 *)(p + 4 * (64 * c + lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * c + i] = (float)t[i];
+    }
+    if (VPL % 4) {
+        const f16x2 t = *(const f16x2 *)(p + 256 * N4 + 2 * lane);
+        v[4 * N4] = (float)t[0];
+        v[4 * N4 + 1] = (float)t[1];
+    }
+}
+template <int VPL>
+__device__ __forceinline__ void st_row(float *o32, f16 *o16, int lane, const float (&y)[VPL]) {
+    constexpr int N4 = VPL / 4;
+#pragma unroll
+    for (int c = 0; c < N4; ++c) {
+        const int e = 4 * (64 * c + lane);
+        if (o32) *(f32x4 *)(o32 + e) = (f32x4){y[4 * c], y[4 * c + 1], y[4 * c + 2], y[4 * c + 3]};
+        *(f16x4 *)(o16 + e) = (f16x4){(f16)y[4 * c], (f16)y[4 * c + 1], (f16)y[4 * c + 2], (f16)y[4 * c + 3]};
+    }
+    if (VPL % 4) {
+        const int e = 256 * N4 + 2 * lane;
+        if (o32) *(f32x2 *)(o32 + e) = (f32x2){y[4 * N4], y[4 * N4 + 1]};
+        *(f16x2 *)(o16 + e) = (f16x2){(f16)y[4 * N4], (f16)y[4 * N4 + 1]};
+    }
 }
 
 template <int VPL>
@@ -158,29 +208,24 @@ __device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float *gamma, co
     }
     const float var = wave_sum_f32(q) * (1.0f / H);
     const float inv = 1.0f / sqrtf(var + eps);
+    float gw[VPL], gb[VPL];
+    ld_row<VPL>(gamma, lane, gw);
+    ld_row<VPL>(beta, lane, gb);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int e = lane + 64 * j;
-        const float y = (v[j] - mean) * inv * gamma[e] + beta[e];
-        if (o32) o32[e] = y;
-        o16[e] = (f16)y;
-    }
+    for (int j = 0; j < VPL; ++j) v[j] = (v[j] - mean) * inv * gw[j] + gb[j];
+    st_row<VPL>(o32, o16, lane, v);
 }
-
-template <int VPL>
-__global__ __launch_bounds__(256) void layer_norm_v_kernel(const float *y, int M, const float *gamma,
+template <int VPL, class T>
+__global__ __launch_bounds__(256) void layer_norm_v_kernel(const T *y, int M, const float *gamma,
                                                            const float *beta, float eps, float *x32, f16 *x16) {
     constexpr int H = 64 * VPL;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const int lane = threadIdx.x & 63;
-    const float *src = y + (size_t)row * H;
     float v[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) v[j] = src[lane + 64 * j];
+    ld_row<VPL>(y + (size_t)row * H, lane, v);
     ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 + (size_t)row * H);
 }
-
 template <int VPL>
 __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, const int32_t *offsets,
                                                          const float *word, const float *type0, const float *pos,
@@ -193,15 +238,17 @@ __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, con
     if (t >= L) return;
     const int lane = threadIdx.x & 63;
     const size_t row = (size_t)(start + t);
-    const float *w = word + (size_t)ids[row] * H;
-    float v[VPL];
+    float v[VPL], u[VPL];
+    ld_row<VPL>(word + (size_t)ids[row] * H, lane, v);
+    if (type0) {
+        ld_row<VPL>(type0, lane, u);
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int e = lane + 64 * j;
-        float x = w[e];
-        if (type0) x += type0[e];
-        if (pos) x += pos[(size_t)t * H + e];
-        v[j] = x;
+        for (int j = 0; j < VPL; ++j) v[j] += u[j];
+    }
+    if (pos) {
+        ld_row<VPL>(pos + (size_t)t * H, lane, u);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) v[j] += u[j];
     }
     ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
 }
@@ -295,12 +342,16 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
                        x32, x16);
     return hipGetLastError();
 }
-hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const float *beta, float eps,
-                      float *x32, f16 *x16, hipStream_t s) {
+hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
+                      float eps, float *x32, f16 *x16, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const dim3 grid((M + 3) / 4);
-#define FH_LN_V(V)                                                                                          \
-    case V: hipLaunchKernelGGL(layer_norm_v_kernel<V>, grid, dim3(256), 0, s, y, M, gamma, beta, eps, x32, x16); \
+#define FH_LN_V(V)                                                                                             \
+    case V:                                                                                                    \
+        if (y16) hipLaunchKernelGGL((layer_norm_v_kernel<V, f16>), grid, dim3(256), 0, s, y16, M, gamma, beta, eps, \
+                                    x32, x16);                                                                 \
+        else hipLaunchKernelGGL((layer_norm_v_kernel<V, float>), grid, dim3(256), 0, s, y32, M, gamma, beta, eps, \
+                                x32, x16);                                                                     \
         return hipGetLastError();
     if (H % 64 == 0 && gamma && x16) {
         switch (H / 64) {
@@ -309,7 +360,8 @@ hipError_t layer_norm(const float *y, int M, int H, const float *gamma, const fl
         }
     }
 #undef FH_LN_V
-    hipLaunchKernelGGL(layer_norm_kernel, grid, dim3(256), 0, s, y, M, H, gamma, beta, eps, x32, x16);
+    if (y16) hipLaunchKernelGGL(layer_norm_kernel<f16>, grid, dim3(256), 0, s, y16, M, H, gamma, beta, eps, x32, x16);
+    else hipLaunchKernelGGL(layer_norm_kernel<float>, grid, dim3(256), 0, s, y32, M, H, gamma, beta, eps, x32, x16);
     return hipGetLastError();
 }
 hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,

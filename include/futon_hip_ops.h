@@ -26,12 +26,14 @@ extern "C" {
 
 /* C[M,N'] = act(A[M,K] · B[N,K]ᵀ (· sA[m]·sB[n] for I8) + bias[N]) + resid[M,N'],
  * N' = N (N/2 for SwiGLU).  Output f32 when out_f32, else binary16.
+ * resid is f32, or binary16 when resid_f16 (F16, no activation, binary16
+ * output only: the sum is formed in f32 and rounded once).
  * Requires K % 16 == 0 for I8, K % 8 == 0 for F16, N % 4 == 0 (N % 32 for SwiGLU).
  * Replaces: Kernel.MatMulT / MatMulTF16 (native/kernel.go:26-43) and
  * q8Kernel.MatMulTQ8 (native/quant.go:92-137). */
-int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const float *resid,
-               const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N, int32_t K,
-               int32_t act, int32_t out_f32, void *stream);
+int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, const void *resid,
+               int32_t resid_f16, const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N,
+               int32_t K, int32_t act, int32_t out_f32, void *stream);
 
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,
@@ -42,10 +44,11 @@ int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32
                     int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
                     int32_t q_limit, int32_t compact, int32_t out_f32, void *stream);
 
-/* x32/x16[M,H] = LN(y) with γ, β (NULL γ = parameter-free).
+/* x32/x16[M,H] = LN(y) with γ, β (NULL γ = parameter-free); y is f32, or
+ * binary16 when y_f16.
  * Replaces: layerNormRows (native/model.go:743-769). */
-int fh_op_layer_norm(const float *y, int32_t M, int32_t H, const float *gamma, const float *beta,
-                     float eps, float *x32, void *x16, void *stream);
+int fh_op_layer_norm(const void *y, int32_t y_f16, int32_t M, int32_t H, const float *gamma,
+                     const float *beta, float eps, float *x32, void *x16, void *stream);
 
 /* Per-row int8 codes + scales of x[M,K] (row stride K).
  * Replaces: quantizeRowQ8 over activation rows (native/quant.go:42-70, :104-110). */

@@ -39,8 +39,9 @@ def gemm(dtype, A, B, bias=None, resid=None, a_scale=None, b_scale=None, act=0, 
     N = B.shape[0]
     nout = N // 2 if act == 2 else N
     C = torch.empty((M, nout), dtype=torch.float32 if out_f32 else torch.float16, device="cuda")
-    rc = _lib().fh_op_gemm(dtype, ptr(A), ptr(B), ptr(bias), ptr(resid), ptr(a_scale), ptr(b_scale), ptr(C),
-                           M, N, K, act, int(out_f32), None)
+    resid_f16 = int(resid is not None and resid.dtype == torch.float16)
+    rc = _lib().fh_op_gemm(dtype, ptr(A), ptr(B), ptr(bias), ptr(resid), resid_f16, ptr(a_scale), ptr(b_scale),
+                           ptr(C), M, N, K, act, int(out_f32), None)
     assert rc == 0
     sync()
     return C.cpu().numpy()
@@ -70,6 +71,22 @@ def test_gemm_f16_matches_float64(M, N, K):
     np.testing.assert_allclose(got_g, gelu64(ref), atol=2e-4 * math.sqrt(K), rtol=1e-5)
     got_h = gemm(0, dev(a), dev(b), None, out_f32=False).astype(np.float64)
     np.testing.assert_allclose(got_h, ref - bias, atol=2e-3 * math.sqrt(K) / 8, rtol=1e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 64, 32), (130, 384, 384), (257, 384, 1536), (300, 768, 768), (129, 132, 40)])
+def test_gemm_f16_residual_rounds_once(M, N, K):
+    """Binary16 output with a binary16 residual: bias and residual are added
+    in f32 and the sum is rounded once, so the result is within half an f16
+    ulp (plus the f32 accumulation error) of the exact value."""
+    rng = np.random.default_rng(M + N + K)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    b = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = (rng.standard_normal((M, N)) * 2).astype(np.float16)
+    ref = a.astype(np.float64) @ b.astype(np.float64).T + bias + resid.astype(np.float64)
+    got = gemm(0, dev(a), dev(b), dev(bias), dev(resid), out_f32=False).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 0.5 * ulp + 2e-5 * math.sqrt(K)), np.abs(got - ref).max()
 
 
 @pytest.mark.parametrize("M,I,K", [(5, 32, 32), (70, 256, 64), (200, 1536, 384)])
@@ -195,16 +212,19 @@ def test_attention_matches_float64(H, heads, lens, rope):
     np.testing.assert_allclose(outc.cpu().numpy(), ref[offsets[:-1]], atol=3e-3, rtol=3e-3)
 
 
-@pytest.mark.parametrize("M,H", [(1, 32), (9, 384), (100, 768), (3, 1024)])
-def test_layer_norm_matches_oracle(M, H):
+@pytest.mark.parametrize("y_f16", [0, 1])
+@pytest.mark.parametrize("M,H", [(1, 32), (9, 384), (100, 768), (3, 1024), (5, 256), (7, 160)])
+def test_layer_norm_matches_oracle(M, H, y_f16):
     rng = np.random.default_rng(M + H)
     y = (rng.standard_normal((M, H)) * 3 + 0.5).astype(np.float32)
+    if y_f16:
+        y = y.astype(np.float16).astype(np.float32)  # the kernel reads binary16 values exactly
     g = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
     b = (0.02 * rng.standard_normal(H)).astype(np.float32)
     x32 = torch.empty((M, H), dtype=torch.float32, device="cuda")
     x16 = torch.empty((M, H), dtype=torch.float16, device="cuda")
-    dy, dg, db = dev(y), dev(g), dev(b)
-    assert _lib().fh_op_layer_norm(ptr(dy), M, H, ptr(dg), ptr(db), 1e-12, ptr(x32), ptr(x16), None) == 0
+    dy, dg, db = dev(y.astype(np.float16) if y_f16 else y), dev(g), dev(b)
+    assert _lib().fh_op_layer_norm(ptr(dy), y_f16, M, H, ptr(dg), ptr(db), 1e-12, ptr(x32), ptr(x16), None) == 0
     sync()
     want = oracle.layer_norm_rows(y, g, b, 1e-12)
     np.testing.assert_allclose(x32.cpu().numpy(), want, atol=2e-6, rtol=0)
