@@ -122,6 +122,10 @@ struct DevLayer {
     DevMat qkv, out, ffn1, fc2;  // ffn1 = fc1, or fc1|gate interleaved in 16-row blocks (SwiGLU)
     float *qkv_b = nullptr, *out_b = nullptr, *ffn1_b = nullptr, *fc2_b = nullptr;
     float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+    // LayerNorm folding (binary16 path): qkv/ffn1 weights are stored scaled by
+    // the γ of the LayerNorm feeding them; c1 = row sums of those stored
+    // weights, c2 = W·β + bias (float64 sums).
+    float *qkv_c1 = nullptr, *qkv_c2 = nullptr, *ffn1_c1 = nullptr, *ffn1_c2 = nullptr;
 };
 
 enum KClass {
@@ -144,6 +148,7 @@ struct ProfPending {
 struct fh_model {
     fh_config cfg{};
     int device = 0, hd = 0, eff_max = 0;
+    bool lnfold = false;  // LayerNorms folded into the GEMMs (binary16 path)
     hipStream_t stream = nullptr;
     float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -161,6 +166,8 @@ struct fh_model {
     int8_t *xq = nullptr;
     float *xs = nullptr;
     int32_t *ids = nullptr, *offsets = nullptr;
+    f32x2 *sA = nullptr, *sB = nullptr, *sAc = nullptr, *sBc = nullptr;  // per-row (mean, rstd)
+    f16 *yBc = nullptr;
     // Pinned host staging for fh_encode.
     void *pin = nullptr;
     size_t pin_bytes = 0;
@@ -264,6 +271,18 @@ struct Loader {
         tv.to_f32(h);
         return upload(m, dst, h.data(), h.size() * 4);
     }
+    int vec_host(const std::string &name, int64_t len, std::vector<float> &h, bool optional = false) {
+        TensorView tv;
+        bool present = true;
+        int rc = need(name, {len}, tv, optional, &present);
+        if (rc) return rc;
+        if (!present) {
+            h.clear();
+            return FH_OK;
+        }
+        tv.to_f32(h);
+        return FH_OK;
+    }
     int mat_f32(const std::string &name, int64_t r, int64_t c, float **dst) {
         TensorView tv;
         int rc = need(name, {r, c}, tv);
@@ -280,6 +299,27 @@ struct Loader {
         return FH_OK;
     }
 };
+
+// LayerNorm folding of a GEMM fed by LN(y) = (y − mean)·rstd·γ + β:
+// x·Wᵀ + b = rstd·(y·W'ᵀ − mean·c1) + c2 with W' = f16(W·diag(γ)),
+// c1[n] = Σ_k W'[n,k] (of the stored binary16 values, so the mean term
+// cancels exactly what y·W'ᵀ contains) and c2[n] = Σ_k W[n,k]·β[k] + b[n].
+void fold_ln(std::vector<float> &w, int n, int k, const std::vector<float> &g, const std::vector<float> &beta,
+             const std::vector<float> &bias, std::vector<float> &c1, std::vector<float> &c2) {
+    c1.assign((size_t)n, 0.f);
+    c2.assign((size_t)n, 0.f);
+    for (int r = 0; r < n; r++) {
+        float *row = &w[(size_t)r * k];
+        double s1 = 0.0, s2 = bias.empty() ? 0.0 : (double)bias[(size_t)r];
+        for (int j = 0; j < k; j++) {
+            s2 += (double)row[j] * (double)beta[(size_t)j];
+            row[j] = f16_to_f32(f32_to_f16(row[j] * g[(size_t)j]));
+            s1 += (double)row[j];
+        }
+        c1[(size_t)r] = (float)s1;
+        c2[(size_t)r] = (float)s2;
+    }
+}
 
 // Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales.
 int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8) {
@@ -332,6 +372,9 @@ int ensure_workspace(fh_model *m, int tokens, int seqs) {
         {(void **)&m->xc32, (size_t)S * H * 4},       {(void **)&m->xc16, (size_t)S * H * 2},
         {(void **)&m->attnc, (size_t)S * H * hsz},    {(void **)&m->out, (size_t)S * H * 4},
         {(void **)&m->ids, (size_t)T * 4},            {(void **)&m->offsets, (size_t)(S + 1) * 4},
+        {(void **)&m->sA, (size_t)T * 8},             {(void **)&m->sB, (size_t)T * 8},
+        {(void **)&m->sAc, (size_t)S * 8},            {(void **)&m->sBc, (size_t)S * 8},
+        {(void **)&m->yBc, (size_t)S * H * 2},
     };
     if (q8) {
         plan.push_back({(void **)&m->xq, (size_t)T * std::max(H, I)});
@@ -456,6 +499,60 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     return FH_OK;
 }
 
+// Binary16 GEMM whose A operand is the un-normalized input y of a folded
+// LayerNorm (LN_IN): C = act(rstd·(y·W'ᵀ − mean·c1) + c2); the row statistics
+// of y go to stats_out.
+int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const float *c1, const float *c2,
+              f32x2 *stats_out, void *C, int ldc, int act, hipStream_t s) {
+    GemmArgs g{};
+    g.A = y;
+    g.B = w.w;
+    g.C = C;
+    g.M = M;
+    g.N = w.n;
+    g.K = w.k;
+    g.lda = w.k;
+    g.ldb = w.k;
+    g.ldc = ldc;
+    g.c1 = c1;
+    g.c2 = c2;
+    g.stats_out = stats_out;
+    g.ln_eps = (float)m->cfg.layer_norm_eps;
+    const double flops = 2.0 * M * (double)w.n * w.k;
+    const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
+    const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + (stats_out ? M * 8.0 : 0.0);
+    Scope sc(m, cls, flops, bytes, s);
+    LCHK(fh::gemm_f16(g, act, false, s, fh::LN_IN));
+    return FH_OK;
+}
+
+// Binary16 GEMM with the residual LN(yr) rebuilt in the epilogue (RES_LN):
+// C = f16(A·Wᵀ + bias + (yr − mean)·rstd·γ + β).
+int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, const float *bias, const f16 *yr,
+               const f32x2 *stats, const float *gamma, const float *beta, f16 *C, hipStream_t s) {
+    GemmArgs g{};
+    g.A = A;
+    g.B = w.w;
+    g.bias = bias;
+    g.resid_h = yr;
+    g.C = C;
+    g.M = M;
+    g.N = w.n;
+    g.K = w.k;
+    g.lda = w.k;
+    g.ldb = w.k;
+    g.ldc = w.n;
+    g.ldr = w.n;
+    g.stats_in = stats;
+    g.ln_g = gamma;
+    g.ln_b = beta;
+    const double flops = 2.0 * M * (double)w.n * w.k;
+    const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * w.n * 4 + M * 8.0;
+    Scope sc(m, cls, flops, bytes, s);
+    LCHK(fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
+    return FH_OK;
+}
+
 int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s, int cls = K_QUANT) {
     Scope sc(m, cls, 0.0, (double)M * K * 5, s);
     LCHK(fh::quantize_rows(x, M, K, ldx, m->xq, m->xs, s));
@@ -470,7 +567,94 @@ int layer_norm(fh_model *m, int cls, const float *y32, const f16 *y16, int M, co
     return FH_OK;
 }
 
+// Forward with every LayerNorm but the last folded into the GEMMs (binary16
+// path).  The residual stream is carried un-normalized: yA (x16) is the input
+// of the LayerNorm that feeds the attention block (the embedding sum, then
+// each layer's y2), yB (y32's storage) the input of norm1.  The QKV and FFN1
+// GEMMs normalize on the fly (LN_IN) and record (mean, rstd) per row; the
+// output projection and FC2 rebuild their residual LN(y) from those (RES_LN)
+// and write the next un-normalized y.  Only the last layer's norm2 runs as a
+// kernel, producing the f32 rows pooling reads.
+int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
+    const fh_config &c = m->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
+    const bool cls = c.pooling == FH_POOL_CLS, swiglu = c.activation == FH_ACT_SWIGLU;
+    f16 *const yB = (f16 *)m->y32;
+    int cp = 0, rc;
+    {
+        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + 2) + T * 4.0, s);
+        LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, nullptr, nullptr, 0.f, H,
+                          nullptr, m->x16, s));
+    }
+    for (int li = 0; li < c.num_layers; li++) {
+        const DevLayer &L = m->layers[(size_t)li];
+        if ((rc = checkpoint(m, b, cp, s))) return rc;
+        const bool last = li == c.num_layers - 1, last_cls = cls && last;
+        const float *gA = li ? m->layers[(size_t)li - 1].n2w : m->emb_w;
+        const float *bA = li ? m->layers[(size_t)li - 1].n2b : m->emb_b;
+
+        // qkv = LN(yA)·Wqkvᵀ + b  (model.go:555)
+        if ((rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
+                            s)))
+            return rc;
+
+        // attention (model.go:557-593, 646-701)
+        AttnArgs a{};
+        a.qkv = m->qkv;
+        a.offsets = b.d_offsets;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.out = last_cls ? m->attnc : m->attn;
+        a.H = H;
+        a.d = m->hd;
+        a.ldo = H;
+        a.q_limit = last_cls ? 1 : INT_MAX;
+        a.compact = last_cls ? 1 : 0;
+        a.scale_log2e = (float)(1.0 / std::sqrt((double)m->hd)) * 1.4426950408889634f;
+        {
+            const double nq_l = last_cls ? (double)T : b.sum_l2;
+            Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * 2,
+                     s);
+            LCHK(fh::attention(a, S, b.max_len, false, s));
+        }
+
+        const int M = last_cls ? S : T;
+        f16 *yA = last_cls ? m->xc16 : m->x16, *yBo = last_cls ? m->yBc : yB;
+        f32x2 *sA = last_cls ? m->sAc : m->sA, *sB = last_cls ? m->sBc : m->sB;
+        if (last_cls) {
+            Scope sc(m, K_CLS_TAIL, 0.0, (double)S * (H * 4 + 16), s);
+            LCHK(fh::gather_rows(nullptr, m->x16, m->sA, b.d_offsets, S, H, nullptr, m->xc16, m->sAc, s));
+        }
+        const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1;
+        const int kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
+
+        // yB = attn·Woᵀ + b + LN(yA)  (model.go:596-599)
+        if ((rc = gemm_resln(m, kOut, L.out, last_cls ? m->attnc : m->attn, M, L.out_b, yA, sA, gA, bA, yBo, s)))
+            return rc;
+        if ((rc = checkpoint(m, b, cp, s))) return rc;
+
+        // h = act(LN1(yB)·W1ᵀ + b1); yA = h·W2ᵀ + b2 + LN1(yB)  (model.go:607-633)
+        if ((rc = gemm_lnin(m, kFfn1, L.ffn1, yBo, M, L.ffn1_c1, L.ffn1_c2, sB, m->hbuf, I,
+                            swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU, s)))
+            return rc;
+        if ((rc = gemm_resln(m, kFc2, L.fc2, m->hbuf, M, L.fc2_b, yBo, sB, L.n1w, L.n1b, yA, s))) return rc;
+    }
+    // The last norm2, to f32 rows for pooling.
+    const DevLayer &Lz = m->layers.back();
+    if ((rc = layer_norm(m, K_LN, nullptr, cls ? m->xc16 : m->x16, cls ? S : T, Lz.n2w, Lz.n2b, cls ? m->xc32 : m->x32,
+                         nullptr, s)))
+        return rc;
+    {
+        const int od = b.out_dim == 0 ? H : b.out_dim;
+        Scope sc(m, K_POOL, 0.0, (cls ? (double)S * H * 4 : (double)T * H * 4) + (double)S * od * 4, s);
+        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, H, cls ? 1 : 0, cls ? 0 : 1, c.matryoshka_layernorm,
+                      od, c.normalize, b.d_out, s));
+    }
+    return FH_OK;
+}
+
 int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
+    if (m->lnfold) return run_forward_fold(m, b, s);
     const fh_config &c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
     const bool q8 = c.q8 != 0, cls = c.pooling == FH_POOL_CLS, swiglu = c.activation == FH_ACT_SWIGLU;
@@ -531,8 +715,8 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const void *attn_in = last_cls ? m->attnc : m->attn;
         if (last_cls) {
             Scope sc(m, K_CLS_TAIL, 0.0, (double)S * H * (f32res ? 8 : 4), s);
-            LCHK(fh::gather_rows(f32res ? m->x32 : nullptr, f32res ? nullptr : m->x16, b.d_offsets, S, H,
-                                 f32res ? m->xc32 : nullptr, f32res ? nullptr : m->xc16, s));
+            LCHK(fh::gather_rows(f32res ? m->x32 : nullptr, f32res ? nullptr : m->x16, nullptr, b.d_offsets, S, H,
+                                 f32res ? m->xc32 : nullptr, f32res ? nullptr : m->xc16, nullptr, s));
         }
         const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kLn = last_cls ? K_CLS_TAIL : K_LN;
         const int kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1, kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
@@ -683,41 +867,76 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     if ((rc = ld.vec_f32("embeddings.norm.bias", H, &m->emb_b))) return bail(rc);
 
     const bool swiglu = c.activation == FH_ACT_SWIGLU, q8 = c.q8 != 0;
+    // Fold the LayerNorms into the GEMMs on the binary16 path for the row
+    // widths the un-normalized embedding kernel covers; FUTON_LN_FOLD=0 keeps
+    // the separate LayerNorm kernels (diagnostics).
+    const char *fold_env = getenv("FUTON_LN_FOLD");
+    m->lnfold = !q8 && H % 64 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16) &&
+                !(fold_env && fold_env[0] == '0');
+    std::vector<float> gA, bA, g1, b1, bias, c1, c2;
+    if (m->lnfold && ((rc = ld.vec_host("embeddings.norm.weight", H, gA)) ||
+                      (rc = ld.vec_host("embeddings.norm.bias", H, bA))))
+        return bail(rc);
     m->layers.resize((size_t)c.num_layers);
     std::vector<float> w, g, packed;
     for (int li = 0; li < c.num_layers; li++) {
         DevLayer &L = m->layers[(size_t)li];
         auto nm = [&](const char *s) { return "layers." + std::to_string(li) + "." + s; };
-        if ((rc = ld.mat_host(nm("attn.qkv.weight"), 3 * H, H, w)) || (rc = upload_mat(m, L.qkv, w, 3 * H, H, q8)))
-            return bail(rc);
+        if ((rc = ld.mat_host(nm("attn.qkv.weight"), 3 * H, H, w))) return bail(rc);
+        if (m->lnfold) {
+            if ((rc = ld.vec_host(nm("attn.qkv.bias"), 3 * H, bias, true))) return bail(rc);
+            fold_ln(w, 3 * H, H, gA, bA, bias, c1, c2);
+            if ((rc = upload(m, &L.qkv_c1, c1.data(), c1.size() * 4)) ||
+                (rc = upload(m, &L.qkv_c2, c2.data(), c2.size() * 4)))
+                return bail(rc);
+        }
+        if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8))) return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.qkv.bias"), 3 * H, &L.qkv_b, true))) return bail(rc);
         if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) || (rc = upload_mat(m, L.out, w, H, H, q8)))
             return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.out.bias"), H, &L.out_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm1.weight"), H, &L.n1w)) || (rc = ld.vec_f32(nm("norm1.bias"), H, &L.n1b)))
             return bail(rc);
+        if (m->lnfold &&
+            ((rc = ld.vec_host(nm("norm1.weight"), H, g1)) || (rc = ld.vec_host(nm("norm1.bias"), H, b1))))
+            return bail(rc);
         if ((rc = ld.mat_host(nm("mlp.fc1.weight"), I, H, w))) return bail(rc);
         if (swiglu) {
             if ((rc = ld.mat_host(nm("mlp.gate.weight"), I, H, g))) return bail(rc);
             interleave16(w, g, I, H, packed);
-            if ((rc = upload_mat(m, L.ffn1, packed, 2 * I, H, q8))) return bail(rc);
             // biases follow the same interleave (absent biases stay absent)
             TensorView tb1, tb2;
             bool p1 = false, p2 = false;
             if ((rc = ld.need(nm("mlp.fc1.bias"), {I}, tb1, true, &p1)) ||
                 (rc = ld.need(nm("mlp.gate.bias"), {I}, tb2, true, &p2)))
                 return bail(rc);
+            std::vector<float> bp;
             if (p1 || p2) {
-                std::vector<float> b1((size_t)I, 0.f), b2((size_t)I, 0.f), bp((size_t)2 * I);
-                if (p1) tb1.to_f32(b1);
-                if (p2) tb2.to_f32(b2);
+                std::vector<float> bu((size_t)I, 0.f), bg((size_t)I, 0.f);
+                bp.resize((size_t)2 * I);
+                if (p1) tb1.to_f32(bu);
+                if (p2) tb2.to_f32(bg);
                 for (int r = 0; r < 2 * I; r++) {
                     const int blk = r / 32, ww = r % 32;
-                    bp[(size_t)r] = ww < 16 ? b1[(size_t)(16 * blk + ww)] : b2[(size_t)(16 * blk + ww - 16)];
+                    bp[(size_t)r] = ww < 16 ? bu[(size_t)(16 * blk + ww)] : bg[(size_t)(16 * blk + ww - 16)];
                 }
                 if ((rc = upload(m, &L.ffn1_b, bp.data(), bp.size() * 4))) return bail(rc);
             }
+            if (m->lnfold) {
+                fold_ln(packed, 2 * I, H, g1, b1, bp, c1, c2);
+                if ((rc = upload(m, &L.ffn1_c1, c1.data(), c1.size() * 4)) ||
+                    (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
+                    return bail(rc);
+            }
+            if ((rc = upload_mat(m, L.ffn1, packed, 2 * I, H, q8))) return bail(rc);
         } else {
+            if (m->lnfold) {
+                if ((rc = ld.vec_host(nm("mlp.fc1.bias"), I, bias, true))) return bail(rc);
+                fold_ln(w, I, H, g1, b1, bias, c1, c2);
+                if ((rc = upload(m, &L.ffn1_c1, c1.data(), c1.size() * 4)) ||
+                    (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
+                    return bail(rc);
+            }
             if ((rc = upload_mat(m, L.ffn1, w, I, H, q8))) return bail(rc);
             if ((rc = ld.vec_f32(nm("mlp.fc1.bias"), I, &L.ffn1_b, true))) return bail(rc);
         }
@@ -725,6 +944,9 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
             return bail(rc);
         if ((rc = ld.vec_f32(nm("mlp.fc2.bias"), H, &L.fc2_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm2.weight"), H, &L.n2w)) || (rc = ld.vec_f32(nm("norm2.bias"), H, &L.n2b)))
+            return bail(rc);
+        if (m->lnfold &&
+            ((rc = ld.vec_host(nm("norm2.weight"), H, gA)) || (rc = ld.vec_host(nm("norm2.bias"), H, bA))))
             return bail(rc);
     }
     for (int i = 0; i < n_tensors; i++) {

@@ -37,6 +37,14 @@ struct GemmArgs {
     int M, N, K;
     int lda, ldb, ldc, ldr;
     int epi_lds;         // set by the launcher: stage the epilogue through LDS
+    // LayerNorm folded into the binary16 GEMMs (A and resid_h hold the
+    // un-normalized LN input y; x = (y − mean)·rstd·γ + β is never stored):
+    const float *c1;     // LN_IN: [N] Σ_k B[n,k] (B = W·diag(γ), as stored)
+    const float *c2;     // LN_IN: [N] Σ_k W[n,k]·β[k] + bias[n]
+    f32x2 *stats_out;    // LN_IN: [M] (mean, rstd) of A's rows, or null
+    float ln_eps;        // LN_IN
+    const f32x2 *stats_in;      // RES_LN: [M] (mean, rstd) of resid_h's rows
+    const float *ln_g, *ln_b;   // RES_LN: γ, β of resid_h's LayerNorm
 };
 
 struct AttnArgs {
@@ -56,17 +64,25 @@ namespace fh {
 // ACT_RES16 is internal to the GEMM launcher: no activation, binary16 output
 // with a binary16 residual added in f32 before the single rounding.
 enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_RES16 = 3 };
-hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
+// LayerNorm folding of a binary16 GEMM: LN_IN — A is the LN input y, B the
+// weights scaled by γ, and the epilogue forms rstd·(acc − mean·c1) + c2 with
+// row statistics gathered while A streams through; RES_LN — the residual is
+// LN(resid_h) rebuilt from stats_in, γ, β (binary16 output with ACT_NONE).
+enum LnMode { LN_NONE = 0, LN_IN = 1, RES_LN = 2 };
+hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);
 hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
+// gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
+// binary16 sum to x16 instead, for a consumer that folds this LayerNorm.
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s);
 // y32 or y16 (exactly one non-null) holds proj + bias + residual.
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
                       float eps, float *x32, f16 *x16, hipStream_t s);
-hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,
-                       f16 *xc16, hipStream_t s);
+// Sequence i's first row (and its (mean, rstd) when st is non-null) → row i.
+hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const int32_t *offsets, int nseq, int H,
+                       float *xc32, f16 *xc16, f32x2 *stc, hipStream_t s);
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
                          hipStream_t s);
 hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact,

@@ -39,9 +39,8 @@ struct Cfg {
     static_assert(ACH * NT == BM * (KB / 16) && BCH * NT == BN * (KB / 16), "tile/thread mismatch");
 };
 
-// erf-GELU, 0.5·x·(1 + erf(x/√2)), through the branch-free Numerical Recipes
-// erfc fit the reference uses (native/mathf32.go:73-107; fractional error
-// < 1.2e-7), with the hardware exp.
+// erf-GELU, 0.5·x·(1 + erf(x/√2)) (native/mathf32.go:96-107), with the
+// hardware reciprocal and exp.
 __device__ __forceinline__ float gelu_erf(float x) {
     // x·Φ(x) with erfc(z) = t·P(t)·exp(−z²), t = 1/(1 + p·z), z = |x|/√2
     // (Abramowitz & Stegun 7.1.26, |error| ≤ 1.5e-7).  Constants folded:
@@ -79,9 +78,30 @@ __device__ __forceinline__ void tile_coords(int &mt, int &nt) {
     nt = logical - mt * gx;
 }
 
-template <int ACT, bool OUT_F32>
+// LN_IN fold of one 4-column group: rstd·(acc − mean·c1) + c2.
+__device__ __forceinline__ f32x4 ln_fold(const GemmArgs &g, int col, f32x4 v, f32x2 rs) {
+    const f32x4 c1 = *(const f32x4 *)(g.c1 + col), c2 = *(const f32x4 *)(g.c2 + col);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = rs[1] * (v[i] - rs[0] * c1[i]) + c2[i];
+    return v;
+}
+// RES_LN residual of 4 columns: (y − mean)·rstd·γ + β.
+__device__ __forceinline__ f32x4 ln_resid(const GemmArgs &g, int row, int col, f16x4 y) {
+    const f32x2 st = g.stats_in[row];
+    const f32x4 gm = *(const f32x4 *)(g.ln_g + col), bt = *(const f32x4 *)(g.ln_b + col);
+    f32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = ((float)y[i] - st[0]) * st[1] * gm[i] + bt[i];
+    return r;
+}
+
+template <int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int col, f32x4 v,
-                                               f32x4 gate) {
+                                               f32x4 gate, f32x2 rs) {
+    if (LNM == fh::LN_IN) {
+        v = ln_fold(g, col, v, rs);
+        if (ACT == fh::ACT_SWIGLU) gate = ln_fold(g, col + 16, gate, rs);
+    }
     if (ACT == fh::ACT_SWIGLU) {
         // col is the packed up-column; output column folds the 16-row interleave.
         const int ocol = ((col >> 5) << 4) + (col & 15);
@@ -109,7 +129,8 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
         v += *(const f32x4 *)(g.resid + (size_t)row * g.ldr + col);
     } else if (g.resid_h) {
         const f16x4 r = *(const f16x4 *)(g.resid_h + (size_t)row * g.ldr + col);
-        v += (f32x4){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+        if (LNM == fh::RES_LN) v += ln_resid(g, row, col, r);
+        else v += (f32x4){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
     }
     if (OUT_F32) {
         *(f32x4 *)((float *)g.C + (size_t)row * g.ldc + col) = v;
@@ -121,13 +142,16 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
 
 // Epilogue over a wave's tiles.  Lane holds C[row][col .. col+3] for
 // row = tile_m + lane%16, col = tile_n + (lane/16)·4.
-template <class C, bool I8, int ACT, bool OUT_F32>
+template <class C, bool I8, int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
-                                            const f32x4 (&acc)[C::NTL][C::MT], const i32x4 (&iacc)[C::NTL][C::MT]) {
+                                            const f32x4 (&acc)[C::NTL][C::MT], const i32x4 (&iacc)[C::NTL][C::MT],
+                                            const f32x2 *rowstat) {
 #pragma unroll
     for (int tm = 0; tm < C::MT; ++tm) {
-        const int row = m0 + (wm * C::MT + tm) * 16 + (lane & 15);
+        const int rl = (wm * C::MT + tm) * 16 + (lane & 15);
+        const int row = m0 + rl;
         if (row >= g.M) continue;
+        const f32x2 rs = LNM == fh::LN_IN ? rowstat[rl] : (f32x2){0.f, 0.f};
         float sa = 0.f;
         if (I8) sa = g.a_scale[row];
 #pragma unroll
@@ -150,7 +174,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, i
                 v = acc[tn][tm];
                 if (ACT == fh::ACT_SWIGLU) gate = acc[tn + 1][tm];
             }
-            epilogue_store<ACT, OUT_F32>(g, row, col, v, gate);
+            epilogue_store<ACT, OUT_F32, LNM>(g, row, col, v, gate, rs);
         }
     }
 }
@@ -161,10 +185,11 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, i
 // own LDS region, then writes whole row segments with 16-byte stores, adding
 // the residual in the same coalesced pass.  Needs 64 output columns per wave
 // (32 for SwiGLU) and the operand LDS free (after the K loop's last barrier).
-template <class C, bool I8, int ACT, bool OUT_F32>
+template <class C, bool I8, int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
                                                 int wave, const f32x4 (&acc)[C::NTL][C::MT],
-                                                const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds) {
+                                                const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds,
+                                                const f32x2 *rowstat) {
     static_assert(C::NTL * 16 == 64 && C::MT % 2 == 0, "staged epilogue expects 64-column wave tiles");
     constexpr int OC = ACT == fh::ACT_SWIGLU ? 32 : 64;  // output columns per wave
     constexpr bool R16 = ACT == fh::ACT_RES16;
@@ -178,7 +203,9 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int tm = 2 * p + h;
-            const int row = m0 + (wm * C::MT + tm) * 16 + (lane & 15);
+            const int rl = (wm * C::MT + tm) * 16 + (lane & 15);
+            const int row = m0 + rl;
+            const f32x2 rs = LNM == fh::LN_IN ? rowstat[rl] : (f32x2){0.f, 0.f};
             float sa = 0.f;
             if (I8) sa = g.a_scale[min(row, g.M - 1)];
 #pragma unroll
@@ -199,6 +226,10 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 } else {
                     v = acc[tn][tm];
                     if (ACT == fh::ACT_SWIGLU) gate = acc[tn + 1][tm];
+                }
+                if (LNM == fh::LN_IN) {
+                    v = ln_fold(g, col, v, rs);
+                    if (ACT == fh::ACT_SWIGLU) gate = ln_fold(g, col + 16, gate, rs);
                 }
                 if (ACT == fh::ACT_SWIGLU) {
                     if (g.bias) {
@@ -234,13 +265,26 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 const f32x4 hi = *(const f32x4 *)(region + r * RS + ch * 32 + 16);
                 if (grow >= g.M) continue;
                 const int gcol = ocol0 + ch * 8;
-                f16x8 rr = {};
-                if (g.resid_h) rr = *(const f16x8 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = r0;
+                if (g.resid_h) {
+                    const f16x8 rr = *(const f16x8 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                    const f16x4 ra = {rr[0], rr[1], rr[2], rr[3]}, rb = {rr[4], rr[5], rr[6], rr[7]};
+                    if (LNM == fh::RES_LN) {
+                        r0 = ln_resid(g, grow, gcol, ra);
+                        r1 = ln_resid(g, grow, gcol + 4, rb);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            r0[i] = (float)ra[i];
+                            r1[i] = (float)rb[i];
+                        }
+                    }
+                }
                 f16x8 o;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    o[i] = (f16)(lo[i] + (float)rr[i]);
-                    o[4 + i] = (f16)(hi[i] + (float)rr[4 + i]);
+                    o[i] = (f16)(lo[i] + r0[i]);
+                    o[4 + i] = (f16)(hi[i] + r1[i]);
                 }
                 *(f16x8 *)((f16 *)g.C + (size_t)grow * g.ldc + gcol) = o;
             }
@@ -269,7 +313,15 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
     }
 }
 
-template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32>
+// DPP sum over each aligned group of 8 lanes (xor 1, xor 2, half-row mirror).
+__device__ __forceinline__ float sum8_lanes(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    return v;
+}
+
+template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
 __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) uint8_t As[2][C::BM * C::ROW];
     __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
@@ -325,11 +377,29 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
             }
         }
     };
-    auto sstore = [&](int st, int buf) {
+    // LN_IN: Σy and Σy² of this thread's 8-element pieces of its A rows, over
+    // the slices it stores (each stored exactly once); f16 products are exact.
+    float ssum[C::ACH], ssq[C::ACH];
+#pragma unroll
+    for (int i = 0; i < C::ACH; ++i) ssum[i] = ssq[i] = 0.f;
+    auto sstore = [&](int st, int buf, bool fresh) {
 #pragma unroll
         for (int i = 0; i < C::ACH; ++i) {
             const int c = tid + i * C::NT;
             *(i32x4 *)&As[buf][(c >> 3) * C::ROW + (c & 7) * 16] = ra[st][i];
+        }
+        if (LNM == fh::LN_IN && fresh) {
+            const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+            for (int i = 0; i < C::ACH; ++i) {
+                const f16x8 h = __builtin_bit_cast(f16x8, ra[st][i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f16x2 pr = {h[2 * j], h[2 * j + 1]};
+                    ssum[i] = __builtin_amdgcn_fdot2(pr, one, ssum[i], false);
+                    ssq[i] = __builtin_amdgcn_fdot2(pr, pr, ssq[i], false);
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < C::BCH; ++i) {
@@ -381,14 +451,14 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
     if (C::PF == 1) {
         // One register stage: slice kt+1 is fetched while slice kt is multiplied.
         gload(0, 0);
-        sstore(0, 0);
+        sstore(0, 0, true);
         lds_barrier();
         for (int kt = 0; kt < nk; ++kt) {
             gload(0, min((kt + 1) * KB, last));
             __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
             compute(kt & 1);
             __builtin_amdgcn_sched_barrier(0);
-            sstore(0, (kt + 1) & 1);
+            sstore(0, (kt + 1) & 1, kt + 1 < nk);
             lds_barrier();
         }
     } else {
@@ -399,12 +469,12 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_barrier(0);     // keep the prefetch ahead of the MFMAs
             compute(par);
             __builtin_amdgcn_sched_barrier(0);
-            sstore(par ^ 1, par ^ 1);
+            sstore(par ^ 1, par ^ 1, kt + 1 < nk);
             lds_barrier();
         };
         gload(0, 0);
         gload(1, min(KB, last));
-        sstore(0, 0);
+        sstore(0, 0, true);
         lds_barrier();
         int kt = 0;
         for (; kt + 1 < nk; kt += 2) {
@@ -414,170 +484,78 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
         if (kt < nk) step(kt, 0);
     }
 
-    static_assert((C::NT / 64) * 32 * (64 * 4 + 16) <= 2 * C::BM * C::ROW, "epilogue staging exceeds LDS");
-    if (KFULL && g.epi_lds)
-        store_tiles_lds<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0]);
-    else
-        store_tiles<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, acc, iacc);
-}
-
-// Variant for large M: only the weight tile goes through LDS.  Waves are
-// stacked along M, and each wave loads its activation fragments straight
-// from global memory into registers in the MFMA operand layout (lane reads
-// 16 bytes of row lane%16 at K offset (lane/16)·16), one slice ahead.  This
-// removes the activation tile's LDS write and read traffic, which otherwise
-// saturates the LDS pipe before the MFMA pipe.
-template <class C, bool I8, int ACT, bool OUT_F32>
-__global__ __launch_bounds__(C::NT) void gemm_adirect_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / C::WN, wn = wave % C::WN;
-    int mt, nt;
-    tile_coords(mt, nt);
-    const int m0 = mt * C::BM, n0 = nt * C::BN;
-    constexpr int ESZ = I8 ? 1 : 2;
-    const int kbytes = g.K * ESZ;
-    const uint8_t *A = (const uint8_t *)g.A;
-    const uint8_t *B = (const uint8_t *)g.B;
-    const size_t lda = (size_t)g.lda * ESZ, ldb = (size_t)g.ldb * ESZ;
-
-    const uint8_t *arow[C::MT];
+    // Row statistics sit past the epilogue staging area of the A buffers.
+    static_assert((C::NT / 64) * 32 * (64 * 4 + 16) + C::BM * 8 <= 2 * C::BM * C::ROW, "epilogue staging exceeds LDS");
+    f32x2 *rowstat = (f32x2 *)(&As[0][0] + 2 * C::BM * C::ROW - C::BM * 8);
+    if (LNM == fh::LN_IN) {
+        const float invk = 1.0f / (float)g.K;
 #pragma unroll
-    for (int t = 0; t < C::MT; ++t) {
-        const int r = min(m0 + (wm * C::MT + t) * 16 + (lane & 15), g.M - 1);
-        arow[t] = A + (size_t)r * lda + (lane >> 4) * 16;
-    }
-    const uint8_t *bsrc[C::BCH];
-#pragma unroll
-    for (int i = 0; i < C::BCH; ++i) {
-        const int c = tid + i * C::NT;
-        bsrc[i] = B + (size_t)min(n0 + (c >> 3), g.N - 1) * ldb + (c & 7) * 16;
-    }
-
-    i32x4 af[2][C::MT][2];  // [stage][m tile][k step]
-    i32x4 rb[C::BCH];
-    auto aload = [&](int st, int kb0) {
-#pragma unroll
-        for (int t = 0; t < C::MT; ++t)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) af[st][t][ks] = *(const i32x4 *)(arow[t] + kb0 + ks * 64);
-    };
-    auto bload = [&](int kb0) {
-#pragma unroll
-        for (int i = 0; i < C::BCH; ++i) rb[i] = *(const i32x4 *)(bsrc[i] + kb0);
-    };
-    auto bstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < C::BCH; ++i) {
-            const int c = tid + i * C::NT;
-            *(i32x4 *)&Bs[buf][(c >> 3) * C::ROW + (c & 7) * 16] = rb[i];
+        for (int i = 0; i < C::ACH; ++i) {
+            const float s = sum8_lanes(ssum[i]), q = sum8_lanes(ssq[i]);
+            const int rl = (tid + i * C::NT) >> 3;
+            if ((tid & 7) == 0) {
+                const float mean = s * invk;
+                const float var = fmaxf(q * invk - mean * mean, 0.f);
+                const f32x2 st = {mean, 1.0f / sqrtf(var + g.ln_eps)};
+                rowstat[rl] = st;
+                if (g.stats_out && nt == 0 && m0 + rl < g.M) g.stats_out[m0 + rl] = st;
+            }
         }
-    };
-
-    f32x4 acc[C::NTL][C::MT];
-    i32x4 iacc[C::NTL][C::MT];
-    const i32x4 zero = {0, 0, 0, 0};
-#pragma unroll
-    for (int a = 0; a < C::NTL; ++a)
-#pragma unroll
-        for (int b = 0; b < C::MT; ++b) {
-            acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            iacc[a][b] = zero;
-        }
-
-    const int nk = kbytes / KB;  // launcher guarantees K·ESZ % 128 == 0
-    const int last = (nk - 1) * KB;
-    const int brow0 = (wn * C::NTL * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
-    auto compute = [&](int par) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            i32x4 bf[C::NTL];
-#pragma unroll
-            for (int t = 0; t < C::NTL; ++t) bf[t] = *(const i32x4 *)&Bs[par][brow0 + t * 16 * C::ROW + ks * 64];
-#pragma unroll
-            for (int tn = 0; tn < C::NTL; ++tn)
-#pragma unroll
-                for (int tm = 0; tm < C::MT; ++tm) {
-                    if (I8) {
-                        iacc[tn][tm] =
-                            __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[tn], af[par][tm][ks], iacc[tn][tm], 0, 0, 0);
-                    } else {
-                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[par][tm][ks]),
-                            acc[tn][tm], 0, 0, 0);
-                    }
-                }
-        }
-    };
-    // Slice kt: activations in register stage kt%2, weights in LDS buffer
-    // kt%2.  Weight loads for kt+1 are issued before activation loads so the
-    // wait before the LDS store leaves the activation loads in flight.
-    auto step = [&](int kt, int par) {
-        const int nxt = min((kt + 1) * KB, last);
-        bload(nxt);
-        aload(par ^ 1, nxt);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(par);
-        __builtin_amdgcn_sched_barrier(0);
-        bstore(par ^ 1);
         lds_barrier();
-    };
-    bload(0);
-    aload(0, 0);
-    bstore(0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        step(kt, 0);
-        step(kt + 1, 1);
     }
-    if (kt < nk) step(kt, 0);
-
-    store_tiles<C, I8, ACT, OUT_F32>(g, m0, n0, wm, wn, lane, acc, iacc);
+    if (KFULL && g.epi_lds)
+        store_tiles_lds<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0], rowstat);
+    else
+        store_tiles<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, acc, iacc, rowstat);
 }
 
 // Tile configurations (block tile, wave grid, row pad, prefetch depth).
-// 0–3 stage both operands through LDS; 4–6 stage only the weights.
 using C0 = Cfg<128, 128, 2, 2, 16, 1>;
 using C1 = Cfg<128, 128, 2, 2, 32, 1>;
 using C2 = Cfg<256, 128, 4, 2, 32, 1>;
 using C3 = Cfg<256, 128, 4, 2, 32, 2>;
-using C4 = Cfg<256, 128, 4, 2, 32, 1>;
 using C5 = Cfg<256, 256, 2, 4, 32, 1>;
-using C6 = Cfg<256, 128, 4, 2, 32, 1>;
+
+template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
+void launch_one(const GemmArgs &g, hipStream_t s) {
+    dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
+    hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, ACT, OUT_F32, LNM>), grid, dim3(C::NT), 0, s, g);
+}
 
 template <class C, bool I8, bool KFULL>
-hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
-    dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
-    dim3 block(C::NT);
-    if (act == fh::ACT_NONE && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_NONE, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_NONE) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_NONE, true>), grid, block, 0, s, g);
-    else if (act == fh::ACT_GELU && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_GELU, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_GELU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_GELU, true>), grid, block, 0, s, g);
-    else if (act == fh::ACT_SWIGLU && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_SWIGLU) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_SWIGLU, true>), grid, block, 0, s, g);
-    else if (act == fh::ACT_RES16 && !out_f32) hipLaunchKernelGGL((gemm_kernel<C, I8, KFULL, fh::ACT_RES16, false>), grid, block, 0, s, g);
-    else return hipErrorInvalidValue;
+hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, int ln, hipStream_t s) {
+    if (ln != fh::LN_NONE) {  // binary16 only
+        if constexpr (I8) {
+            return hipErrorInvalidValue;
+        } else if (ln == fh::LN_IN && KFULL && !out_f32) {
+            if (act == fh::ACT_NONE) launch_one<C, false, KFULL, fh::ACT_NONE, false, fh::LN_IN>(g, s);
+            else if (act == fh::ACT_GELU) launch_one<C, false, KFULL, fh::ACT_GELU, false, fh::LN_IN>(g, s);
+            else if (act == fh::ACT_SWIGLU) launch_one<C, false, KFULL, fh::ACT_SWIGLU, false, fh::LN_IN>(g, s);
+            else return hipErrorInvalidValue;
+        } else if (ln == fh::RES_LN && !out_f32 && act == fh::ACT_RES16) {
+            launch_one<C, false, KFULL, fh::ACT_RES16, false, fh::RES_LN>(g, s);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else if (act == fh::ACT_NONE) {
+        if (out_f32) launch_one<C, I8, KFULL, fh::ACT_NONE, true, fh::LN_NONE>(g, s);
+        else launch_one<C, I8, KFULL, fh::ACT_NONE, false, fh::LN_NONE>(g, s);
+    } else if (act == fh::ACT_GELU) {
+        if (out_f32) launch_one<C, I8, KFULL, fh::ACT_GELU, true, fh::LN_NONE>(g, s);
+        else launch_one<C, I8, KFULL, fh::ACT_GELU, false, fh::LN_NONE>(g, s);
+    } else if (act == fh::ACT_SWIGLU) {
+        if (out_f32) launch_one<C, I8, KFULL, fh::ACT_SWIGLU, true, fh::LN_NONE>(g, s);
+        else launch_one<C, I8, KFULL, fh::ACT_SWIGLU, false, fh::LN_NONE>(g, s);
+    } else if (act == fh::ACT_RES16 && !out_f32) {
+        launch_one<C, I8, KFULL, fh::ACT_RES16, false, fh::LN_NONE>(g, s);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-template <class C, bool I8>
-hipError_t launch_adirect(const GemmArgs &g, int act, bool out_f32, hipStream_t s) {
-    dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM);
-    dim3 block(C::NT);
-    if (act == fh::ACT_NONE && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_NONE, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_NONE) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_NONE, true>), grid, block, 0, s, g);
-    else if (act == fh::ACT_GELU && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_GELU, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_GELU) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_GELU, true>), grid, block, 0, s, g);
-    else if (act == fh::ACT_SWIGLU && !out_f32) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_SWIGLU, false>), grid, block, 0, s, g);
-    else if (act == fh::ACT_SWIGLU) hipLaunchKernelGGL((gemm_adirect_kernel<C, I8, fh::ACT_SWIGLU, true>), grid, block, 0, s, g);
-    else return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-// FUTON_GEMM_TILE=0..6 pins a configuration (tuning knob); otherwise the
-// choice depends only on the problem shape.
+// FUTON_GEMM_TILE=0,1,2,3,5 pins a configuration (tuning knob); otherwise
+// the choice depends only on the problem shape.
 int forced_cfg() {
     static const int v = [] {
         const char *e = getenv("FUTON_GEMM_TILE");
@@ -587,7 +565,7 @@ int forced_cfg() {
 }
 
 template <bool I8>
-hipError_t launch(const GemmArgs &ga, int act, bool out_f32, hipStream_t s) {
+hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t s) {
     if (ga.M <= 0) return hipSuccess;
     GemmArgs g = ga;
     if (act == fh::ACT_NONE && !out_f32 && g.resid_h && !g.resid) act = fh::ACT_RES16;
@@ -596,9 +574,10 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, hipStream_t s) {
     g.epi_lds = (nout % (act == fh::ACT_SWIGLU ? 32 : 64) == 0) && (g.N % 64 == 0) &&
                 (out_f32 || act == fh::ACT_RES16 || !has_res) && (g.ldc % 8 == 0) && (!has_res || g.ldr % 8 == 0);
     const bool kfull = (g.K * (I8 ? 1 : 2)) % KB == 0;
-    if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, s);
+    if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // statistics need whole 128-byte slices
+    if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, ln, s);
     int cfg = forced_cfg();
-    if (cfg < 0 || cfg > 6) {
+    if (cfg < 0 || cfg > 5 || cfg == 4) {
         // 256×256 when it still gives every CU a block; 256×128 down to half
         // the CUs (it beats 128×128 on the N = H projections even there).
         const long m256 = (g.M + 255) / 256;
@@ -607,23 +586,21 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, hipStream_t s) {
         else cfg = 0;
     }
     switch (cfg) {
-    case 1: return launch_cfg<C1, I8, true>(g, act, out_f32, s);
-    case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, s);
-    case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, s);
-    case 4: return launch_adirect<C4, I8>(g, act, out_f32, s);
-    case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, s);
-    case 6: return launch_cfg<C6, I8, true>(g, act, out_f32, s);
-    default: return launch_cfg<C0, I8, true>(g, act, out_f32, s);
+    case 1: return launch_cfg<C1, I8, true>(g, act, out_f32, ln, s);
+    case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, ln, s);
+    case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, ln, s);
+    case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, ln, s);
+    default: return launch_cfg<C0, I8, true>(g, act, out_f32, ln, s);
     }
 }
 
 }  // namespace
 
 namespace fh {
-hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s) {
-    return launch<false>(a, act, out_f32, s);
+hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln) {
+    return launch<false>(a, act, out_f32, ln, s);
 }
 hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s) {
-    return launch<true>(a, act, out_f32, s);
+    return launch<true>(a, act, out_f32, fh::LN_NONE, s);
 }
 }  // namespace fh

@@ -95,10 +95,11 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T *y, int M, int 
 
 // xc[i] = x[offsets[i]]: the CLS rows the last layer computes (model.go:403-410),
 // from the f32 and/or f16 stream.
-__global__ void gather_rows_kernel(const float *x32, const f16 *x16, const int32_t *offsets, int H, float *xc32,
-                                   f16 *xc16) {
+__global__ void gather_rows_kernel(const float *x32, const f16 *x16, const f32x2 *st, const int32_t *offsets, int H,
+                                   float *xc32, f16 *xc16, f32x2 *stc) {
     const int seq = blockIdx.x;
     const size_t src = (size_t)offsets[seq] * H, dst = (size_t)seq * H;
+    if (st && threadIdx.x == 0) stc[seq] = st[offsets[seq]];
     for (int e = threadIdx.x; e < H; e += blockDim.x) {
         if (x32) xc32[dst + e] = x32[src + e];
         if (x16) xc16[dst + e] = x16[src + e];
@@ -139,10 +140,23 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *x, int 
 // 16/8-byte (f32) or 8/4-byte (f16) vector and a wave covers contiguous
 // memory.  Statistics in float32, two-pass (mean, then centered variance),
 // which keeps the relative error of the normalized values near 1e-7.
+// Wave sum without LDS traffic: DPP butterflies inside each 16-lane row
+// (xor 1, xor 2, half-row mirror, row mirror leave the row sum in every lane
+// of the row), then the four row sums read out as scalars.
+template <int CTRL>
+__device__ __forceinline__ float dpp_step(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v = dpp_step<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_step<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_step<0x141>(v);  // row_half_mirror
+    v = dpp_step<0x140>(v);  // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
 template <int VPL>
@@ -182,17 +196,19 @@ __device__ __forceinline__ void st_row(float *o32, f16 *o16, int lane, const flo
     for (int c = 0; c < N4; ++c) {
         const int e = 4 * (64 * c + lane);
         if (o32) *(f32x4 *)(o32 + e) = (f32x4){y[4 * c], y[4 * c + 1], y[4 * c + 2], y[4 * c + 3]};
-        *(f16x4 *)(o16 + e) = (f16x4){(f16)y[4 * c], (f16)y[4 * c + 1], (f16)y[4 * c + 2], (f16)y[4 * c + 3]};
+        if (o16) *(f16x4 *)(o16 + e) = (f16x4){(f16)y[4 * c], (f16)y[4 * c + 1], (f16)y[4 * c + 2], (f16)y[4 * c + 3]};
     }
     if (VPL % 4) {
         const int e = 256 * N4 + 2 * lane;
         if (o32) *(f32x2 *)(o32 + e) = (f32x2){y[4 * N4], y[4 * N4 + 1]};
-        *(f16x2 *)(o16 + e) = (f16x2){(f16)y[4 * N4], (f16)y[4 * N4 + 1]};
+        if (o16) *(f16x2 *)(o16 + e) = (f16x2){(f16)y[4 * N4], (f16)y[4 * N4 + 1]};
     }
 }
 
+// Normalizes v in place with statistics of the row and writes it out; gw/gb
+// hold this lane's γ/β elements.
 template <int VPL>
-__device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float *gamma, const float *beta, float eps,
+__device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL], const float (&gb)[VPL], float eps,
                                          float *o32, f16 *o16) {
     constexpr int H = 64 * VPL;
     const int lane = threadIdx.x & 63;
@@ -208,23 +224,30 @@ __device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float *gamma, co
     }
     const float var = wave_sum_f32(q) * (1.0f / H);
     const float inv = 1.0f / sqrtf(var + eps);
-    float gw[VPL], gb[VPL];
-    ld_row<VPL>(gamma, lane, gw);
-    ld_row<VPL>(beta, lane, gb);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) v[j] = (v[j] - mean) * inv * gw[j] + gb[j];
     st_row<VPL>(o32, o16, lane, v);
 }
+
+// Two rows per wave: both rows and γ/β are requested before any reduction,
+// so one memory latency covers the pair.
 template <int VPL, class T>
 __global__ __launch_bounds__(256) void layer_norm_v_kernel(const T *y, int M, const float *gamma,
                                                            const float *beta, float eps, float *x32, f16 *x16) {
     constexpr int H = 64 * VPL;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
     if (row >= M) return;
+    const bool two = row + 1 < M;
     const int lane = threadIdx.x & 63;
-    float v[VPL];
-    ld_row<VPL>(y + (size_t)row * H, lane, v);
-    ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 + (size_t)row * H);
+    float v0[VPL], v1[VPL], gw[VPL], gb[VPL];
+    ld_row<VPL>(y + (size_t)row * H, lane, v0);
+    if (two) ld_row<VPL>(y + (size_t)(row + 1) * H, lane, v1);
+    ld_row<VPL>(gamma, lane, gw);
+    ld_row<VPL>(beta, lane, gb);
+    ln_row_v<VPL>(v0, gw, gb, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 ? x16 + (size_t)row * H : nullptr);
+    if (two)
+        ln_row_v<VPL>(v1, gw, gb, eps, x32 ? x32 + (size_t)(row + 1) * H : nullptr,
+                      x16 ? x16 + (size_t)(row + 1) * H : nullptr);
 }
 template <int VPL>
 __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, const int32_t *offsets,
@@ -250,7 +273,14 @@ __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, con
 #pragma unroll
         for (int j = 0; j < VPL; ++j) v[j] += u[j];
     }
-    ln_row_v<VPL>(v, gamma, beta, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
+    if (!gamma) {  // un-normalized sum, for a consumer that folds this LayerNorm
+        st_row<VPL>(nullptr, x16 + row * H, lane, v);
+        return;
+    }
+    float gw[VPL], gb[VPL];
+    ld_row<VPL>(gamma, lane, gw);
+    ld_row<VPL>(beta, lane, gb);
+    ln_row_v<VPL>(v, gw, gb, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
 }
 
 __device__ double block_sum_f64(double v, double *red) {
@@ -345,15 +375,15 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
                       float eps, float *x32, f16 *x16, hipStream_t s) {
     if (M <= 0) return hipSuccess;
-    const dim3 grid((M + 3) / 4);
+    const dim3 grid((M + 3) / 4), grid2((M + 7) / 8);
 #define FH_LN_V(V)                                                                                             \
     case V:                                                                                                    \
-        if (y16) hipLaunchKernelGGL((layer_norm_v_kernel<V, f16>), grid, dim3(256), 0, s, y16, M, gamma, beta, eps, \
+        if (y16) hipLaunchKernelGGL((layer_norm_v_kernel<V, f16>), grid2, dim3(256), 0, s, y16, M, gamma, beta, eps, \
                                     x32, x16);                                                                 \
-        else hipLaunchKernelGGL((layer_norm_v_kernel<V, float>), grid, dim3(256), 0, s, y32, M, gamma, beta, eps, \
+        else hipLaunchKernelGGL((layer_norm_v_kernel<V, float>), grid2, dim3(256), 0, s, y32, M, gamma, beta, eps, \
                                 x32, x16);                                                                     \
         return hipGetLastError();
-    if (H % 64 == 0 && gamma && x16) {
+    if (H % 64 == 0 && gamma) {
         switch (H / 64) {
             FH_LN_V(4) FH_LN_V(6) FH_LN_V(8) FH_LN_V(12) FH_LN_V(16)
         default: break;
@@ -364,10 +394,10 @@ hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const floa
     else hipLaunchKernelGGL(layer_norm_kernel<float>, grid, dim3(256), 0, s, y32, M, H, gamma, beta, eps, x32, x16);
     return hipGetLastError();
 }
-hipError_t gather_rows(const float *x32, const f16 *x16, const int32_t *offsets, int nseq, int H, float *xc32,
-                       f16 *xc16, hipStream_t s) {
+hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const int32_t *offsets, int nseq, int H,
+                       float *xc32, f16 *xc16, f32x2 *stc, hipStream_t s) {
     if (nseq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq), dim3(128), 0, s, x32, x16, offsets, H, xc32, xc16);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq), dim3(128), 0, s, x32, x16, st, offsets, H, xc32, xc16, stc);
     return hipGetLastError();
 }
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
