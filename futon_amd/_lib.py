@@ -1,5 +1,5 @@
-"""ctypes binding of futon_amd/libfuton_hip.so (include/futon_hip.h and
-include/futon_hip_ops.h).  The library is the only compute path: if it is not
+"""ctypes binding of futon_amd/libfuton_hip.so (include/futon_hip.h,
+include/futon_hip_ops.h and include/futon_host.h).  The library is the only compute path: if it is not
 built, importing the model API raises; there is no CPU fallback."""
 from __future__ import annotations
 
@@ -31,6 +31,11 @@ EXPORTED = (
     "fh_strerror", "fh_last_error", "fh_model_device_bytes",
     "fh_op_gemm", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
     "fh_op_pool",
+    "fh_tokenizer_new", "fh_tokenizer_encode", "fh_tokenizer_vocab_size", "fh_tokenizer_free",
+    "fh_pack_load", "fh_pack_config_load", "fh_pack_config", "fh_pack_model_id", "fh_pack_tensor_count",
+    "fh_pack_create_model", "fh_pack_free", "fh_safetensors_check",
+    "fh_provider_new", "fh_provider_embed", "fh_provider_embed_batch", "fh_provider_dimensions",
+    "fh_provider_model_name", "fh_provider_is_available", "fh_provider_close", "fh_provider_free", "fh_futon_new",
 )
 
 
@@ -49,6 +54,13 @@ class FhConfig(ctypes.Structure):
 class FhTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int32), ("rank", ctypes.c_int32),
                 ("shape", ctypes.c_int64 * 4), ("data", ctypes.c_void_p)]
+
+
+class FhTokenizerConfig(ctypes.Structure):
+    _fields_ = [("do_lower_case", ctypes.c_int32), ("tokenize_chinese_chars", ctypes.c_int32),
+                ("max_input_chars_per_word", ctypes.c_int32), ("cls_token", ctypes.c_char_p),
+                ("sep_token", ctypes.c_char_p), ("unk_token", ctypes.c_char_p), ("pad_token", ctypes.c_char_p),
+                ("mask_token", ctypes.c_char_p)]
 
 
 class FutonError(RuntimeError):
@@ -93,6 +105,35 @@ def load():
     L.fh_op_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
     L.fh_op_embed_ln.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, ctypes.c_float, i32, vp, vp, vp]
     L.fh_op_pool.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    cp, sz, pvp = ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(vp)
+    L.fh_tokenizer_new.argtypes = [cp, ctypes.POINTER(FhTokenizerConfig), pvp]
+    L.fh_tokenizer_encode.argtypes = [vp, cp, sz, i32, vp, i32, ctypes.POINTER(i32)]
+    L.fh_tokenizer_vocab_size.restype = i32
+    L.fh_tokenizer_vocab_size.argtypes = [vp]
+    L.fh_tokenizer_free.restype = None
+    L.fh_tokenizer_free.argtypes = [vp]
+    L.fh_pack_load.argtypes = [cp, pvp]
+    L.fh_pack_config_load.argtypes = [cp, ctypes.POINTER(FhConfig), ctypes.POINTER(i32)]
+    L.fh_pack_config.argtypes = [vp, i32, ctypes.POINTER(FhConfig)]
+    L.fh_pack_model_id.argtypes = [vp, cp, sz]
+    L.fh_pack_tensor_count.restype = i32
+    L.fh_pack_tensor_count.argtypes = [vp]
+    L.fh_pack_create_model.argtypes = [vp, i32, i32, pvp]
+    L.fh_pack_free.restype = None
+    L.fh_pack_free.argtypes = [vp]
+    L.fh_safetensors_check.argtypes = [cp, sz, ctypes.POINTER(i32)]
+    L.fh_provider_new.argtypes = [cp, i32, i32, pvp]
+    L.fh_provider_embed.argtypes = [vp, cp, sz, vp, vp]
+    L.fh_provider_embed_batch.argtypes = [vp, vp, vp, i32, vp, vp]
+    L.fh_provider_dimensions.restype = i32
+    L.fh_provider_dimensions.argtypes = [vp]
+    L.fh_provider_model_name.argtypes = [vp, cp, sz]
+    L.fh_provider_is_available.restype = i32
+    L.fh_provider_is_available.argtypes = [vp]
+    L.fh_provider_close.argtypes = [vp]
+    L.fh_provider_free.restype = None
+    L.fh_provider_free.argtypes = [vp]
+    L.fh_futon_new.argtypes = [cp, cp, cp, i32, i32, pvp]
     _lib = L
     return L
 

@@ -1,7 +1,10 @@
-"""Builds futon_amd/libfuton_hip.so (HIP kernels + C ABI) for gfx950 in-tree.
+"""Builds futon_amd/libfuton_hip.so (HIP kernels + C ABI + C++ host layer)
+for gfx950 in-tree.
 
-Each ``csrc/*.hip`` is compiled by hipcc in parallel, then linked into one
-shared library next to this file.  Flags:
+Each ``csrc/*.hip`` is compiled by hipcc and each ``csrc/host/*.cpp`` (the
+host side: pack loading, tokenizer, provider) by the host C++ compiler, in
+parallel; everything is linked into one shared library next to this file.
+Flags:
 
 * ``--offload-arch=gfx950`` — MI355X only; no other targets, no host fallback.
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` — keep the compiler from
@@ -19,6 +22,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfuton_hip.so")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+HOST = os.path.join(CSRC, "host")
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
@@ -27,13 +32,21 @@ FLAGS = [
 ]
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(os.path.dirname(HERE), "include")]
+
+
 def sources() -> list[str]:
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    hip = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    host = sorted(os.path.join(HOST, f) for f in os.listdir(HOST) if f.endswith(".cpp"))
+    return hip + host
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [CXX, *HOST_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -25,20 +25,11 @@
 
 #include "../../include/futon_hip.h"
 #include "fh_common.h"
+#include "host/host_common.h"
 
 namespace {
 
-thread_local std::string g_err;
-
-int fail(int code, const char *fmt, ...) {
-    char buf[1024];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
-    va_end(ap);
-    g_err = buf;
-    return code;
-}
+using fh::fail;
 
 #define HIPCHK(expr)                                                                       \
     do {                                                                                   \
@@ -772,28 +763,6 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
 }  // namespace
 
 // ───────────────────────────── C ABI ─────────────────────────────
-
-extern "C" const char *fh_strerror(int code) {
-    switch (code) {
-    case FH_OK: return "ok";
-    case FH_EINVAL: return "invalid argument";
-    case FH_ENOMEM: return "out of memory";
-    case FH_EHIP: return "HIP runtime error";
-    case FH_ECANCELED: return "canceled";
-    case FH_ETOOLONG: return "sequence too long";
-    case FH_ENODEV: return "no gfx950 device";
-    default: return "unknown error";
-    }
-}
-
-extern "C" int fh_last_error(char *buf, size_t len) {
-    if (buf && len) {
-        size_t n = std::min(len - 1, g_err.size());
-        memcpy(buf, g_err.data(), n);
-        buf[n] = 0;
-    }
-    return (int)g_err.size();
-}
 
 extern "C" void fh_model_destroy(fh_model *m) {
     if (!m) return;

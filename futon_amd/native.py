@@ -1,26 +1,27 @@
-"""Host side of the futon encoder on MI355X, mirroring the reference's
-``native`` package API for the forward path:
+"""Python binding of the host side of the futon encoder on MI355X.
 
+The host side itself is C++ (include/futon_native.hpp, futon_amd/csrc/host):
+pack loading with the reference's validation, the WordPiece tokenizer and
+the Provider.  This module exposes it through the C ABI (include/futon_host.h
+and include/futon_hip.h) under the reference's names, so tests read like the
+reference's own:
+
+* ``LoadPackConfig`` / ``PackConfig``  — native/config.go:54-187
+* ``ParseSafetensors`` / ``LoadSafetensors(Raw)`` — native/safetensors.go:79-221
+* ``LoadPack``                         — the host half of LoadModel, model.go:112-131
 * ``LoadModel(dir, threads)``          — native/model.go:112-132
-* ``Model.Config()``                   — native/model.go:298
-* ``Model.EncodeTokens(ids, out_dim)`` — native/model.go:335-457
-* ``Model.EncodeBatch(batch, out_dim)``— one device call for many sequences,
-                                          what Provider.EmbedBatch drives
-                                          (native/provider.go:152-202)
-* ``PackConfig`` + ``LoadPackConfig``  — native/config.go:54-187
-* ``LoadSafetensors(Raw)``             — native/safetensors.go:79-221
-* manifest verification               — native/manifest.go:46-104
+* ``Model.EncodeTokens`` / ``EncodeBatch`` — native/model.go:335-457
+* ``Tokenizer`` / ``NewTokenizer``     — native/tokenizer.go:94-176
+* ``New`` / ``Provider``               — native/provider.go:70-290
+* ``futon_New``                        — futon.go:84-98
 
-Every validation happens here, on the host, before the C ABI is called —
-the same split the reference's Go host keeps in front of its kernels.  The
-forward itself runs only in libfuton_hip.so; there is no CPU path.
+The forward runs only in libfuton_hip.so; there is no CPU path.
 """
 from __future__ import annotations
 
 import ctypes
 import hashlib
 import json
-import math
 import os
 import struct
 import threading
@@ -37,12 +38,19 @@ POS_ABSOLUTE, POS_ROPE = "absolute", "rope"
 ACT_GELU, ACT_SWIGLU = "gelu", "swiglu"
 POOL_MEAN, POOL_CLS = "mean", "cls"
 ENV_NATIVE_Q8 = "FUTON_NATIVE_Q8"
-MAX_HEADER_BYTES = 16 << 20
-MANIFEST_MEMBERS = ("config.json", "model.safetensors", "vocab.txt")
 
 
 class PackError(ValueError):
     """A pack failed validation (the reference's load-time errors)."""
+
+
+def _raise(rc: int, what: str) -> None:
+    if rc == _lib.FH_OK:
+        return
+    msg = _lib.last_error()
+    if rc == _lib.FH_EINVAL:
+        raise PackError(msg)
+    raise FutonError(rc, f"{what}: {msg}")
 
 
 # ── config (native/config.go) ────────────────────────────────────────────────
@@ -54,6 +62,8 @@ class MatryoshkaConfig:
 
 @dataclass
 class PackConfig:
+    """Field view of a pack's config.json.  Validation is the C++ host
+    layer's (PackConfig::Validate); this object only carries the values."""
     pack_format: int = 0
     model_id: str = ""
     hidden_size: int = 0
@@ -91,133 +101,49 @@ class PackConfig:
             return self.max_trained_positions
         return self.max_seq_len
 
-    def Validate(self) -> None:  # native/config.go:119-171
-        mid = self.model_id
-        if self.pack_format != PACK_FORMAT_VERSION:
-            raise PackError(f"pack: unsupported pack_format {self.pack_format} (loader supports {PACK_FORMAT_VERSION})")
-        if not mid:
-            raise PackError("pack: model_id missing")
-        if self.hidden_size <= 0 or self.num_layers <= 0 or self.num_heads <= 0 or self.intermediate_size <= 0:
-            raise PackError(f"pack {mid}: non-positive architecture dimension")
-        if self.hidden_size % self.num_heads:
-            raise PackError(f"pack {mid}: hidden_size {self.hidden_size} not divisible by num_heads {self.num_heads}")
-        if self.vocab_size <= 0 or self.max_seq_len <= 2:
-            raise PackError(f"pack {mid}: invalid vocab_size/max_seq_len")
-        if self.max_trained_positions < 0 or 0 < self.max_trained_positions <= 2:
-            raise PackError(f"pack {mid}: invalid max_trained_positions {self.max_trained_positions}")
-        if self.layer_norm_eps <= 0:
-            raise PackError(f"pack {mid}: layer_norm_eps must be positive")
-        if self.position_encoding == POS_ROPE:
-            if self.rope_theta <= 0:
-                raise PackError(f"pack {mid}: rope position encoding requires rope_theta > 0")
-        elif self.position_encoding != POS_ABSOLUTE:
-            raise PackError(f"pack {mid}: unknown position_encoding {self.position_encoding!r}")
-        if self.activation not in (ACT_GELU, ACT_SWIGLU):
-            raise PackError(f"pack {mid}: unknown activation {self.activation!r}")
-        if self.pooling not in (POOL_MEAN, POOL_CLS):
-            raise PackError(f"pack {mid}: unknown pooling {self.pooling!r}")
-        if self.pre_norm:
-            raise PackError(f"pack {mid}: pre_norm is declared but not yet implemented — refusing to run the "
-                            "wrong architecture")
-        if self.matryoshka is not None:
-            for d in self.matryoshka.dims:
-                if d <= 0 or d > self.hidden_size:
-                    raise PackError(f"pack {mid}: matryoshka dim {d} outside (0,{self.hidden_size}]")
 
-
-def LoadPackConfig(dir: str) -> PackConfig:  # native/config.go:174-187
-    try:
-        raw = open(os.path.join(dir, "config.json"), "rb").read()
-    except OSError as e:
-        raise PackError(f"pack: read config: {e}") from e
-    try:
-        d = json.loads(raw)
-    except ValueError as e:
-        raise PackError(f"pack: parse config: {e}") from e
-    cfg = PackConfig.from_dict(d)
-    cfg.Validate()
-    return cfg
+def LoadPackConfig(dir: str) -> PackConfig:
+    """native/config.go:174-187 — read and validate (in C++) <dir>/config.json."""
+    L = _lib.load()
+    c = _lib.FhConfig()
+    eff = ctypes.c_int32()
+    _raise(L.fh_pack_config_load(dir.encode(), ctypes.byref(c), ctypes.byref(eff)), "LoadPackConfig")
+    with open(os.path.join(dir, "config.json"), "rb") as f:
+        return PackConfig.from_dict(json.loads(f.read()))
 
 
 # ── safetensors (native/safetensors.go) ──────────────────────────────────────
 def ParseSafetensors(raw: bytes, keep_f16: bool = False) -> dict:
-    """Strict parse: shapes × dtype must match each span, spans must tile the
-    data section exactly (no gap, overlap or trailing bytes)."""
-    if len(raw) < 8:
-        raise PackError(f"safetensors: file too small ({len(raw)} bytes) for header length prefix")
+    """Strict parse of a safetensors image: the C++ reader validates it
+    (shapes × dtype match each span, spans tile the data section exactly),
+    then the tensors are viewed as numpy arrays."""
+    n = ctypes.c_int32()
+    _raise(_lib.load().fh_safetensors_check(raw, len(raw), ctypes.byref(n)), "ParseSafetensors")
     (hl,) = struct.unpack("<Q", raw[:8])
-    if hl > MAX_HEADER_BYTES:
-        raise PackError(f"safetensors: header length {hl} exceeds limit {MAX_HEADER_BYTES}")
-    if len(raw) < 8 + hl:
-        raise PackError(f"safetensors: declared header length {hl} exceeds file size {len(raw)}")
-    try:
-        header = json.loads(raw[8:8 + hl])
-    except ValueError as e:
-        raise PackError(f"safetensors: parse header JSON: {e}") from e
-    if not isinstance(header, dict):
-        raise PackError("safetensors: header is not an object")
+    header = json.loads(raw[8:8 + hl])
     data = memoryview(raw)[8 + hl:]
-    tensors, spans = {}, []
+    out = {}
     for name, e in header.items():
         if name == "__metadata__":
             continue
-        if not isinstance(e, dict):
-            raise PackError(f"safetensors: tensor {name!r}: parse entry: not an object")
-        dt = e.get("dtype")
-        if dt == "F32":
-            esz, npdt = 4, "<f4"
-        elif dt == "F16":
-            esz, npdt = 2, "<f2"
-        else:
-            raise PackError(f"safetensors: tensor {name!r}: unsupported dtype {dt!r} (want F32 or F16)")
-        shape = e.get("shape")
-        offs = e.get("data_offsets")
-        if not isinstance(shape, list) or not all(isinstance(d, int) for d in shape):
-            raise PackError(f"safetensors: tensor {name!r}: parse entry: bad shape")
-        if not isinstance(offs, list) or len(offs) != 2 or not all(isinstance(o, int) for o in offs):
-            raise PackError(f"safetensors: tensor {name!r}: parse entry: bad data_offsets")
-        n = 1
-        for d in shape:
-            if d < 0:
-                raise PackError(f"safetensors: tensor {name!r}: negative dimension {d}")
-            n *= d
-            if n >= 1 << 64:
-                raise PackError(f"safetensors: tensor {name!r}: shape {shape} element count overflows")
-        if n > (2 ** 63 - 1) // esz:
-            raise PackError(f"safetensors: tensor {name!r}: shape {shape} byte size overflows")
-        b, en = offs
-        if b < 0 or en < b or en > len(data):
-            raise PackError(f"safetensors: tensor {name!r}: offsets [{b},{en}) outside data section of "
-                            f"{len(data)} bytes")
-        if en - b != n * esz:
-            raise PackError(f"safetensors: tensor {name!r}: shape {shape} × {dt} needs {n * esz} bytes, "
-                            f"offsets span {en - b}")
-        arr = np.frombuffer(data[b:en], dtype=npdt).reshape(shape)
-        if dt == "F16" and not keep_f16:
-            arr = arr.astype(np.float32)
-        tensors[name] = arr
-        spans.append((b, en, name))
-    spans.sort()
-    cursor = 0
-    for b, en, name in spans:
-        if b != cursor:
-            raise PackError(f"safetensors: tensor {name!r} begins at {b}, expected {cursor} (overlap or gap)")
-        cursor = en
-    if cursor != len(data):
-        raise PackError(f"safetensors: data section is {len(data)} bytes but tensors cover {cursor}")
-    return tensors
+        b, en = e["data_offsets"][:2]
+        arr = np.frombuffer(data[b:en], dtype="<f4" if e["dtype"] == "F32" else "<f2").reshape(e["shape"])
+        out[name] = arr.astype(np.float32) if (e["dtype"] == "F16" and not keep_f16) else arr
+    return out
 
 
 def LoadSafetensors(path: str) -> dict:
-    return ParseSafetensors(open(path, "rb").read())
+    with open(path, "rb") as f:
+        return ParseSafetensors(f.read())
 
 
 def LoadSafetensorsRaw(path: str) -> dict:
-    return ParseSafetensors(open(path, "rb").read(), keep_f16=True)
+    with open(path, "rb") as f:
+        return ParseSafetensors(f.read(), keep_f16=True)
 
 
-# ── manifest (native/manifest.go) ────────────────────────────────────────────
 def sha256_file(path: str) -> str:
+    """Hex SHA-256 of a file (test helper for re-hashing manifests)."""
     h = hashlib.sha256()
     with open(path, "rb") as f:
         for chunk in iter(lambda: f.read(1 << 20), b""):
@@ -225,46 +151,42 @@ def sha256_file(path: str) -> str:
     return h.hexdigest()
 
 
-def load_and_verify_manifest(dir: str) -> dict:
-    try:
-        raw = open(os.path.join(dir, "manifest.json"), "rb").read()
-    except OSError as e:
-        raise PackError(f"pack {dir}: manifest.json unreadable (refusing to load an unverifiable pack): {e}") from e
-    try:
-        man = json.loads(raw)
-    except ValueError as e:
-        raise PackError(f"pack {dir}: manifest.json malformed: {e}") from e
-    members = man.get("members") or {}
-    for member in MANIFEST_MEMBERS:
-        meta = members.get(member)
-        if meta is None:
-            raise PackError(f"pack {dir}: manifest records no entry for {member}")
-        path = os.path.join(dir, member)
+class Pack:
+    """native/model.go:112-131 up to the device: manifest verification,
+    config, model_id agreement, safetensors, tensor-name set — all in C++."""
+
+    def __init__(self, dir: str):
+        self._h = None
+        h = ctypes.c_void_p()
+        _raise(_lib.load().fh_pack_load(dir.encode(), ctypes.byref(h)), "LoadPack")
+        self._h = h.value
+        self.dir = dir
+        with open(os.path.join(dir, "config.json"), "rb") as f:
+            self.config = PackConfig.from_dict(json.loads(f.read()))
+
+    @property
+    def model_id(self) -> str:
+        buf = ctypes.create_string_buffer(512)
+        _lib.load().fh_pack_model_id(self._h, buf, 512)
+        return buf.value.decode()
+
+    def tensor_count(self) -> int:
+        return _lib.load().fh_pack_tensor_count(self._h)
+
+    def close(self) -> None:
+        if self._h is not None:
+            _lib.load().fh_pack_free(self._h)
+            self._h = None
+
+    def __del__(self):
         try:
-            size = os.path.getsize(path)
-        except OSError as e:
-            raise PackError(f"pack {dir}: member {member}: {e}") from e
-        if size != meta.get("size"):
-            raise PackError(f"pack {dir}: member {member} is {size} bytes, manifest records {meta.get('size')}")
-        got = sha256_file(path)
-        if got != meta.get("sha256"):
-            raise PackError(f"pack {dir}: member {member} sha256 {got} does not match manifest {meta.get('sha256')} "
-                            "(tampered or corrupt — rebuild the pack)")
-    return man
+            self.close()
+        except Exception:
+            pass
 
 
-def verify_tensor_names(man: dict, tensors: dict) -> None:
-    want = man.get("tensor_names")
-    if want is None:
-        return
-    got = sorted(tensors)
-    want = sorted(want)
-    mid = man.get("model_id", "")
-    if len(got) != len(want):
-        raise PackError(f"pack {mid}: {len(got)} tensors on disk, manifest records {len(want)} — tensor set drifted")
-    for g, w in zip(got, want):
-        if g != w:
-            raise PackError(f"pack {mid}: tensor set drifted from manifest (first difference: {g!r} vs recorded {w!r})")
+def LoadPack(dir: str) -> Pack:
+    return Pack(dir)
 
 
 # ── model ────────────────────────────────────────────────────────────────────
@@ -328,6 +250,15 @@ class Model:
             _lib.check(rc, "fh_model_create")
         self._h = h.value
         self._lock = threading.Lock()
+
+    @classmethod
+    def _adopt(cls, cfg: PackConfig, handle: int, q8: bool) -> "Model":
+        m = cls.__new__(cls)
+        m._h = handle
+        m.cfg = cfg
+        m.q8 = q8
+        m._lock = threading.Lock()
+        return m
 
     @property
     def handle(self) -> int:
@@ -425,19 +356,148 @@ class Model:
 
 
 def LoadModel(dir: str, threads: int = 0, device: int = 0, q8: Optional[bool] = None) -> Model:
-    """native/model.go:112-132: verify the manifest, load and validate the
-    config, parse the weights strictly, check the recorded tensor-name set,
-    then upload (newModel's shape checks run at the C ABI).  ``threads`` is
-    accepted for API parity; the device decides its own parallelism."""
-    man = load_and_verify_manifest(dir)
-    cfg = LoadPackConfig(dir)
-    if man.get("model_id") != cfg.model_id:
-        raise PackError(f"pack {cfg.model_id}: manifest is for {man.get('model_id')!r} — mixed pack contents")
+    """native/model.go:112-132: the C++ host layer verifies the manifest,
+    loads and validates the config, parses the weights strictly and checks
+    the recorded tensor-name set (LoadPack); newModel's shape checks and the
+    upload run at the C ABI.  ``threads`` is accepted for API parity."""
+    if q8 is None:
+        q8 = os.environ.get(ENV_NATIVE_Q8) == "1"
+    pack = LoadPack(dir)
     try:
-        tensors = LoadSafetensorsRaw(os.path.join(dir, "model.safetensors"))
-    except PackError as e:
-        raise PackError(f"pack {cfg.model_id}: {e}") from e
-    except OSError as e:
-        raise PackError(f"safetensors: read {dir}: {e}") from e
-    verify_tensor_names(man, tensors)
-    return Model(cfg, tensors, device=device, q8=q8)
+        h = ctypes.c_void_p()
+        _raise(_lib.load().fh_pack_create_model(pack._h, int(bool(q8)), device, ctypes.byref(h)), "LoadModel")
+        return Model._adopt(pack.config, h.value, bool(q8))
+    finally:
+        pack.close()
+
+
+# ── tokenizer (native/tokenizer.go) ──────────────────────────────────────────
+class Tokenizer:
+    """native.NewTokenizer / Tokenizer.Encode (native/tokenizer.go:94-176),
+    implemented in C++."""
+
+    def __init__(self, vocab_path: str, cfg: Optional[dict] = None):
+        cfg = cfg or {}
+        c = _lib.FhTokenizerConfig()
+        c.do_lower_case = int(bool(cfg.get("do_lower_case", False)))
+        c.tokenize_chinese_chars = int(bool(cfg.get("tokenize_chinese_chars", False)))
+        c.max_input_chars_per_word = int(cfg.get("max_input_chars_per_word", 0) or 0)
+        self._keep = []
+        for k in ("cls_token", "sep_token", "unk_token", "pad_token", "mask_token"):
+            v = cfg.get(k)
+            if v:
+                b = v.encode()
+                self._keep.append(b)
+                setattr(c, k, b)
+        self._h = None
+        h = ctypes.c_void_p()
+        _raise(_lib.load().fh_tokenizer_new(vocab_path.encode(), ctypes.byref(c), ctypes.byref(h)), "NewTokenizer")
+        self._h = h.value
+
+    def Encode(self, text, max_seq_len: int) -> list:
+        raw = text.encode("utf-8", "surrogatepass") if isinstance(text, str) else bytes(text)
+        L = _lib.load()
+        n = ctypes.c_int32()
+        cap = max(2, min(max_seq_len, 1 << 20))
+        buf = (ctypes.c_int32 * cap)()
+        _raise(L.fh_tokenizer_encode(self._h, raw, len(raw), max_seq_len, buf, cap, ctypes.byref(n)), "Encode")
+        if n.value > cap:
+            buf = (ctypes.c_int32 * n.value)()
+            _raise(L.fh_tokenizer_encode(self._h, raw, len(raw), max_seq_len, buf, n.value, ctypes.byref(n)), "Encode")
+        return list(buf[:n.value])
+
+    def VocabSize(self) -> int:
+        return _lib.load().fh_tokenizer_vocab_size(self._h)
+
+    def close(self) -> None:
+        if self._h is not None:
+            _lib.load().fh_tokenizer_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def NewTokenizer(vocab_path: str, cfg: Optional[dict] = None) -> Tokenizer:
+    return Tokenizer(vocab_path, cfg)
+
+
+# ── provider (native/provider.go) ─────────────────────────────────────────────
+class Provider:
+    """native.New / Provider (native/provider.go:70-290) over the C++
+    host layer: host tokenization, one packed device call per batch chunk."""
+
+    def __init__(self, handle: int):
+        self._h = handle
+
+    def _handle(self) -> int:
+        if self._h is None:
+            raise FutonError(_lib.FH_EINVAL, "native: provider is freed")
+        return self._h
+
+    def Dimensions(self) -> int:
+        return _lib.load().fh_provider_dimensions(self._handle())
+
+    def ModelName(self) -> str:
+        buf = ctypes.create_string_buffer(512)
+        _lib.load().fh_provider_model_name(self._handle(), buf, 512)
+        return buf.value.decode()
+
+    def IsAvailable(self) -> bool:
+        return bool(_lib.load().fh_provider_is_available(self._handle()))
+
+    def Embed(self, text, cancel=None) -> np.ndarray:
+        return self.EmbedBatch([text], cancel)[0]
+
+    def EmbedBatch(self, texts: Sequence, cancel=None) -> np.ndarray:
+        n = len(texts)
+        dim = self.Dimensions()
+        out = np.zeros((n, dim), dtype=np.float32)
+        if n == 0:
+            return out
+        raws = [t.encode("utf-8", "surrogatepass") if isinstance(t, str) else bytes(t) for t in texts]
+        ptrs = (ctypes.c_char_p * n)(*raws)
+        lens = (ctypes.c_size_t * n)(*[len(r) for r in raws])
+        cflag = None
+        if cancel is not None:
+            cflag = cancel if isinstance(cancel, ctypes.c_int32) else ctypes.c_int32(int(bool(cancel)))
+        rc = _lib.load().fh_provider_embed_batch(self._handle(), ptrs, lens, n, out.ctypes.data,
+                                                 ctypes.addressof(cflag) if cflag is not None else None)
+        if rc != _lib.FH_OK:
+            raise FutonError(rc, _lib.last_error())
+        return out
+
+    def Close(self) -> None:
+        if self._h is not None:
+            _lib.load().fh_provider_close(self._h)
+
+    def free(self) -> None:
+        if self._h is not None:
+            _lib.load().fh_provider_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def New(pack_dir: str, dimensions: int = 0, threads: int = 0) -> Provider:
+    """native.New(Options{PackDir, Dimensions, Threads})."""
+    h = ctypes.c_void_p()
+    _raise(_lib.load().fh_provider_new(pack_dir.encode() if pack_dir is not None else None, dimensions, threads,
+                                       ctypes.byref(h)), "native.New")
+    return Provider(h.value)
+
+
+def futon_New(model: str = "", models_dir: str = "", model_path: str = "", dimensions: int = 0,
+              threads: int = 0) -> Provider:
+    """futon.New(Options{Model, ModelsDir, ModelPath, Dimensions, Threads}) for local packs."""
+    h = ctypes.c_void_p()
+    _raise(_lib.load().fh_futon_new(model.encode(), models_dir.encode(), model_path.encode(), dimensions, threads,
+                                    ctypes.byref(h)), "futon.New")
+    return Provider(h.value)

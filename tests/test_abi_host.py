@@ -1,8 +1,8 @@
-"""CPU-side checks of the boundary and the host loader (no GPU compute):
+"""CPU-side checks of the boundary and the C++ host loader (no GPU compute):
 the library loads and exports every function the public headers declare,
 creation without a gfx950 device fails loudly, and the pack loader rejects
 what the reference's loader rejects (native/model_test.go:479-567,
-native/safetensors_test.go:10-152)."""
+native/safetensors_test.go:10-152, native/config.go:119-171)."""
 import json
 import os
 import re
@@ -20,7 +20,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_functions():
     names = set()
-    for h in ("futon_hip.h", "futon_hip_ops.h"):
+    for h in ("futon_hip.h", "futon_hip_ops.h", "futon_host.h"):
         src = open(os.path.join(ROOT, "include", h)).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
         names |= set(re.findall(r"\b(fh_\w+)\s*\(", src))
@@ -69,24 +69,20 @@ def rehash(dir):
 
 
 def validate_pack(dir):
-    """LoadModel up to (not including) the device upload."""
-    man = native.load_and_verify_manifest(dir)
-    cfg = native.LoadPackConfig(dir)
-    if man["model_id"] != cfg.model_id:
-        raise native.PackError("mixed pack contents")
-    t = native.LoadSafetensorsRaw(os.path.join(dir, "model.safetensors"))
-    native.verify_tensor_names(man, t)
-    return cfg, t
+    """LoadModel up to (not including) the device upload, in the C++ host layer."""
+    p = native.LoadPack(dir)
+    return p.config, p.tensor_count()
 
 
 def test_toy_packs_validate():
     for name in ("toy-absolute-gelu", "toy-rope-swiglu"):
-        cfg, t = validate_pack(os.path.join(packio.TOY, name))
-        assert cfg.EffectiveMaxSeqLen() == 64 and len(t) > 10
+        cfg, n = validate_pack(os.path.join(packio.TOY, name))
+        assert cfg.EffectiveMaxSeqLen() == 64 and n > 10
 
 
 @pytest.mark.parametrize("case", ["wrong_format", "prenorm", "edited_config_stale_manifest", "missing_manifest",
-                                  "truncated_weights", "removed_bias_rehashed", "bad_theta", "bad_matryoshka"])
+                                  "truncated_weights", "removed_bias_rehashed", "bad_theta", "bad_matryoshka",
+                                  "string_dim", "mixed_model_id", "stale_tensor_names", "missing_vocab_member"])
 def test_pack_tamper_fails_loudly(tmp_path, case):
     d = copy_pack(tmp_path, "toy-rope-swiglu" if case in ("bad_theta", "bad_matryoshka") else "toy-absolute-gelu")
     cfgp = os.path.join(d, "config.json")
@@ -116,8 +112,34 @@ def test_pack_tamper_fails_loudly(tmp_path, case):
     elif case == "bad_matryoshka":
         mutate_json(cfgp, lambda m: m.update(matryoshka={"layernorm": True, "dims": [64]}))
         rehash(d)
+    elif case == "string_dim":
+        mutate_json(cfgp, lambda m: m.update(hidden_size="32"))
+        rehash(d)
+    elif case == "mixed_model_id":
+        mutate_json(os.path.join(d, "manifest.json"), lambda m: m.update(model_id="other"))
+    elif case == "stale_tensor_names":
+        mutate_json(os.path.join(d, "manifest.json"), lambda m: m["tensor_names"].append("extra.weight"))
+    elif case == "missing_vocab_member":
+        mutate_json(os.path.join(d, "manifest.json"), lambda m: m["members"].pop("vocab.txt"))
     with pytest.raises(native.PackError):
         validate_pack(d)
+
+
+def test_config_decoding_follows_go_json(tmp_path):
+    """encoding/json field semantics: unknown members ignored, null leaves a
+    field unset, keys match case-insensitively, clamp by max_trained_positions."""
+    d = copy_pack(tmp_path, "toy-rope-swiglu")
+    cfgp = os.path.join(d, "config.json")
+
+    def edit(m):
+        m["unknown_field"] = {"x": [1, 2]}
+        m["HIDDEN_SIZE"] = m.pop("hidden_size")
+        m["prefixes"] = None
+        m["max_trained_positions"] = 16
+    mutate_json(cfgp, edit)
+    rehash(d)
+    cfg, n = validate_pack(d)
+    assert cfg.EffectiveMaxSeqLen() == 16 and n > 10
 
 
 def _st(entries, data):
@@ -162,8 +184,8 @@ def test_synthetic_pack_is_deterministic(tmp_path):
     for k in a:
         assert np.array_equal(a[k], b[k])
     d = synth.write_pack(str(tmp_path / "p"), cfg, a)
-    c2, t2 = validate_pack(d)
-    assert c2.model_id == cfg["model_id"] and set(t2) == set(a)
+    c2, n2 = validate_pack(d)
+    assert c2.model_id == cfg["model_id"] and n2 == len(a)
     ids, off = synth.make_batch(42, 64, 16, 128)
     lens = np.diff(off)
     assert lens.min() >= 16 and lens.max() <= 128
