@@ -27,6 +27,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
     constexpr int KS = D + 8;     // K LDS row stride (halves)
     constexpr int VS = KBLK + 8;  // Vᵀ LDS row stride (halves)
     constexpr int NKT = KBLK / 16;
+    static_assert(KBLK % 32 == 0, "PV consumes 32-key chunks");
     __shared__ __attribute__((aligned(16))) f16 Ks[KBLK * KS];
     __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
 
@@ -105,7 +106,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
 
     for (int kb0 = 0; kb0 < L; kb0 += KBLK) {
         if (kb0 > 0) __syncthreads();  // previous block's K/V fully consumed
-        for (int c = tid; c < KBLK * (D / 8); c += WAVES * 64) {
+        // Stage only the key rows the MFMAs read: whole 32-key PV chunks
+        // that hold a valid key (rows past L repeat the last key: finite).
+        const int rows = min(KBLK, (L - kb0 + 31) & ~31);
+        for (int c = tid; c < rows * (D / 8); c += WAVES * 64) {
             const int r = c / (D / 8), ch = c % (D / 8);
             const int key = min(kb0 + r, L - 1);
             const f16 *row = a.qkv + (size_t)(start + key) * ld + head * d + ch * 8;
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
         }
         __syncthreads();
         if (ROPE) {
-            for (int c = tid; c < KBLK * half; c += WAVES * 64) {
+            for (int c = tid; c < rows * half; c += WAVES * 64) {
                 const int r = c / half, i = c % half;
                 const int pos = min(kb0 + r, L - 1);
                 const float cs = a.rope_cos[pos * half + i], sn = a.rope_sin[pos * half + i];

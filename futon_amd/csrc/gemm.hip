@@ -23,20 +23,25 @@
 
 namespace {
 
-constexpr int KB = 128;  // bytes of K per slice (64 f16 or 128 i8)
+constexpr int KFULL_BYTES = 128;  // K (in bytes) multiple every full-slice configuration divides
 
-// PAD: bytes appended to each 128-byte LDS row (the row stride decides the
-// ds_read_b128 bank pattern); PF: register prefetch depth in slices (1 or 2).
-template <int BM_, int BN_, int WM_, int WN_, int PAD_, int PF_>
+// KB: bytes of K per slice (64 or 128); PAD: bytes appended to each LDS row
+// (the row stride decides the ds_read_b128 bank pattern); PF: register
+// prefetch depth in slices (1 or 2).
+// WPE: waves per SIMD the register budget must allow (2 caps a wave at 256
+// registers, AGPRs included).
+template <int BM_, int BN_, int WM_, int WN_, int PAD_, int PF_, int KB_ = 128, int WPE_ = 1>
 struct Cfg {
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PF = PF_;
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PF = PF_, KB = KB_, WPE = WPE_;
+    static constexpr int CPR = KB / 16;  // 16-byte chunks per slice row
     static constexpr int ROW = KB + PAD_;
     static constexpr int NT = 64 * WM * WN;
     static constexpr int MT = BM / WM / 16;  // 16-row MFMA tiles per wave
     static constexpr int NTL = BN / WN / 16; // 16-col MFMA tiles per wave
-    static constexpr int ACH = BM * (KB / 16) / NT;  // 16-byte A chunks per thread per slice
-    static constexpr int BCH = BN * (KB / 16) / NT;
-    static_assert(ACH * NT == BM * (KB / 16) && BCH * NT == BN * (KB / 16), "tile/thread mismatch");
+    static constexpr int ACH = BM * CPR / NT;  // 16-byte A chunks per thread per slice
+    static constexpr int BCH = BN * CPR / NT;
+    static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/thread mismatch");
+    static_assert(KB == 64 || KB == 128, "slice is one or two MFMA k-steps");
 };
 
 // erf-GELU, 0.5·x·(1 + erf(x/√2)) (native/mathf32.go:96-107), with the
@@ -314,15 +319,19 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
 }
 
 // DPP sum over each aligned group of 8 lanes (xor 1, xor 2, half-row mirror).
-__device__ __forceinline__ float sum8_lanes(float v) {
+// (N = 4: xor 1, xor 2 only.)
+template <int N>
+__device__ __forceinline__ float sum_lanes(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if (N == 8)
+        v += __builtin_bit_cast(float,
+                                __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
     return v;
 }
 
 template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
-__global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) uint8_t As[2][C::BM * C::ROW];
     __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
 
@@ -345,12 +354,12 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < C::ACH; ++i) {
         const int c = tid + i * C::NT;
-        asrc[i] = A + (size_t)min(m0 + (c >> 3), g.M - 1) * lda + (c & 7) * 16;
+        asrc[i] = A + (size_t)min(m0 + c / C::CPR, g.M - 1) * lda + (c % C::CPR) * 16;
     }
 #pragma unroll
     for (int i = 0; i < C::BCH; ++i) {
         const int c = tid + i * C::NT;
-        bsrc[i] = B + (size_t)min(n0 + (c >> 3), g.N - 1) * ldb + (c & 7) * 16;
+        bsrc[i] = B + (size_t)min(n0 + c / C::CPR, g.N - 1) * ldb + (c % C::CPR) * 16;
     }
 
     // Two register stages: slice k+2 is fetched while slice k is multiplied
@@ -363,7 +372,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
             if (KFULL) {
                 ra[st][i] = *(const i32x4 *)(asrc[i] + kb0);
             } else {
-                const int kb = kb0 + ((tid + i * C::NT) & 7) * 16;
+                const int kb = kb0 + ((tid + i * C::NT) % C::CPR) * 16;
                 ra[st][i] = kb < kbytes ? *(const i32x4 *)(asrc[i] + kb0) : zero;
             }
         }
@@ -372,7 +381,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
             if (KFULL) {
                 rb[st][i] = *(const i32x4 *)(bsrc[i] + kb0);
             } else {
-                const int kb = kb0 + ((tid + i * C::NT) & 7) * 16;
+                const int kb = kb0 + ((tid + i * C::NT) % C::CPR) * 16;
                 rb[st][i] = kb < kbytes ? *(const i32x4 *)(bsrc[i] + kb0) : zero;
             }
         }
@@ -386,7 +395,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < C::ACH; ++i) {
             const int c = tid + i * C::NT;
-            *(i32x4 *)&As[buf][(c >> 3) * C::ROW + (c & 7) * 16] = ra[st][i];
+            *(i32x4 *)&As[buf][(c / C::CPR) * C::ROW + (c % C::CPR) * 16] = ra[st][i];
         }
         if (LNM == fh::LN_IN && fresh) {
             const f16x2 one = {(f16)1.0f, (f16)1.0f};
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < C::BCH; ++i) {
             const int c = tid + i * C::NT;
-            *(i32x4 *)&Bs[buf][(c >> 3) * C::ROW + (c & 7) * 16] = rb[st][i];
+            *(i32x4 *)&Bs[buf][(c / C::CPR) * C::ROW + (c % C::CPR) * 16] = rb[st][i];
         }
     };
 
@@ -418,6 +427,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
             iacc[a][b] = zero;
         }
 
+    constexpr int KB = C::KB;
     const int nk = (kbytes + KB - 1) / KB;
     const int arow0 = (wm * C::MT * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
     const int brow0 = (wn * C::NTL * 16 + (lane & 15)) * C::ROW + (lane >> 4) * 16;
@@ -491,9 +501,9 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(GemmArgs g) {
         const float invk = 1.0f / (float)g.K;
 #pragma unroll
         for (int i = 0; i < C::ACH; ++i) {
-            const float s = sum8_lanes(ssum[i]), q = sum8_lanes(ssq[i]);
-            const int rl = (tid + i * C::NT) >> 3;
-            if ((tid & 7) == 0) {
+            const float s = sum_lanes<C::CPR>(ssum[i]), q = sum_lanes<C::CPR>(ssq[i]);
+            const int rl = (tid + i * C::NT) / C::CPR;
+            if ((tid % C::CPR) == 0) {
                 const float mean = s * invk;
                 const float var = fmaxf(q * invk - mean * mean, 0.f);
                 const f32x2 st = {mean, 1.0f / sqrtf(var + g.ln_eps)};
@@ -515,6 +525,10 @@ using C1 = Cfg<128, 128, 2, 2, 32, 1>;
 using C2 = Cfg<256, 128, 4, 2, 32, 1>;
 using C3 = Cfg<256, 128, 4, 2, 32, 2>;
 using C5 = Cfg<256, 256, 2, 4, 32, 1>;
+// 4 waves of 128×64 over 64-byte slices: 61 KB of LDS, so two blocks share a
+// CU and one block's epilogue overlaps the other's K loop.
+using C6 = Cfg<256, 128, 2, 2, 16, 1, 64, 2>;
+using C7 = Cfg<256, 128, 2, 2, 16, 2, 64, 2>;
 
 template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
 void launch_one(const GemmArgs &g, hipStream_t s) {
@@ -573,11 +587,11 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     const bool has_res = g.resid || g.resid_h;
     g.epi_lds = (nout % (act == fh::ACT_SWIGLU ? 32 : 64) == 0) && (g.N % 64 == 0) &&
                 (out_f32 || act == fh::ACT_RES16 || !has_res) && (g.ldc % 8 == 0) && (!has_res || g.ldr % 8 == 0);
-    const bool kfull = (g.K * (I8 ? 1 : 2)) % KB == 0;
+    const bool kfull = (g.K * (I8 ? 1 : 2)) % KFULL_BYTES == 0;
     if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // statistics need whole 128-byte slices
     if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, ln, s);
     int cfg = forced_cfg();
-    if (cfg < 0 || cfg > 5 || cfg == 4) {
+    if (cfg < 0 || cfg > 7 || cfg == 4) {
         // 256×256 when it still gives every CU a block; 256×128 down to half
         // the CUs (it beats 128×128 on the N = H projections even there).
         const long m256 = (g.M + 255) / 256;
@@ -590,6 +604,8 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, ln, s);
     case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, ln, s);
     case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, ln, s);
+    case 6: return launch_cfg<C6, I8, true>(g, act, out_f32, ln, s);
+    case 7: return launch_cfg<C7, I8, true>(g, act, out_f32, ln, s);
     default: return launch_cfg<C0, I8, true>(g, act, out_f32, ln, s);
     }
 }
