@@ -25,14 +25,12 @@ namespace {
 
 constexpr int KFULL_BYTES = 128;  // K (in bytes) multiple every full-slice configuration divides
 
-// KB: bytes of K per slice (64 or 128); PAD: bytes appended to each LDS row
-// (the row stride decides the ds_read_b128 bank pattern); PF: register
-// prefetch depth in slices (1 or 2).
-// WPE: waves per SIMD the register budget must allow (2 caps a wave at 256
-// registers, AGPRs included).
-template <int BM_, int BN_, int WM_, int WN_, int PAD_, int PF_, int KB_ = 128, int WPE_ = 1>
+// KB: bytes of K per slice; PAD: bytes appended to each LDS row (the row
+// stride decides the ds_read_b128 bank pattern: 160 bytes reads 16 rows at
+// one offset without conflicts); PF: register prefetch depth in slices.
+template <int BM_, int BN_, int WM_, int WN_, int PAD_, int PF_>
 struct Cfg {
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PF = PF_, KB = KB_, WPE = WPE_;
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, PF = PF_, KB = 128;
     static constexpr int CPR = KB / 16;  // 16-byte chunks per slice row
     static constexpr int ROW = KB + PAD_;
     static constexpr int NT = 64 * WM * WN;
@@ -41,7 +39,6 @@ struct Cfg {
     static constexpr int ACH = BM * CPR / NT;  // 16-byte A chunks per thread per slice
     static constexpr int BCH = BN * CPR / NT;
     static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/thread mismatch");
-    static_assert(KB == 64 || KB == 128, "slice is one or two MFMA k-steps");
 };
 
 // erf-GELU, 0.5·x·(1 + erf(x/√2)) (native/mathf32.go:96-107), with the
@@ -188,21 +185,23 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, i
 // so storing them directly writes 16 rows × 32 bytes per instruction.  Here
 // each wave stages 32 rows of its (after bias/activation/scales) tile in its
 // own LDS region, then writes whole row segments with 16-byte stores, adding
-// the residual in the same coalesced pass.  Needs 64 output columns per wave
-// (32 for SwiGLU) and the operand LDS free (after the K loop's last barrier).
+// the residual in the same coalesced pass.  Needs whole block columns (N a
+// multiple of BN: the launcher checks), a multiple of 32 columns per wave and
+// the operand LDS free (after the K loop's last barrier).
 template <class C, bool I8, int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
                                                 int wave, const f32x4 (&acc)[C::NTL][C::MT],
                                                 const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds,
                                                 const f32x2 *rowstat) {
-    static_assert(C::NTL * 16 == 64 && C::MT % 2 == 0, "staged epilogue expects 64-column wave tiles");
-    constexpr int OC = ACT == fh::ACT_SWIGLU ? 32 : 64;  // output columns per wave
+    static_assert(C::MT % 2 == 0 && C::NTL % 2 == 0, "staged epilogue works on 32-row, 32-column multiples");
+    constexpr int WTN = C::NTL * 16;                           // wave tile width
+    constexpr int OC = ACT == fh::ACT_SWIGLU ? WTN / 2 : WTN;  // output columns per wave
     constexpr bool R16 = ACT == fh::ACT_RES16;
     constexpr int ESZ = (OUT_F32 || R16) ? 4 : 2;        // staged element size (bytes)
     constexpr int RS = OC * ESZ + 16;                    // LDS row stride (bytes)
     constexpr int CPR = OC * ESZ / 16;                   // 16-byte chunks per row
     uint8_t *region = lds + wave * 32 * RS;
-    const int ocol0 = ACT == fh::ACT_SWIGLU ? (n0 + wn * 64) >> 1 : n0 + wn * 64;
+    const int ocol0 = ACT == fh::ACT_SWIGLU ? (n0 + wn * WTN) >> 1 : n0 + wn * WTN;
 #pragma unroll
     for (int p = 0; p < C::MT / 2; ++p) {
 #pragma unroll
@@ -262,9 +261,11 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
         if (R16) {
             // 8 output columns per lane step: two staged f32 chunks plus the
             // binary16 residual, rounded once, one 16-byte store.
+            constexpr int C8 = OC / 8;  // 8-column output chunks per row
+            static_assert((32 * C8) % 64 == 0, "whole lane steps");
 #pragma unroll
-            for (int j = 0; j < 32 * 8 / 64; ++j) {
-                const int c = lane + 64 * j, r = c >> 3, ch = c & 7;
+            for (int j = 0; j < 32 * C8 / 64; ++j) {
+                const int c = lane + 64 * j, r = c / C8, ch = c % C8;
                 const int grow = m0 + (wm * C::MT + 2 * p) * 16 + r;
                 const f32x4 lo = *(const f32x4 *)(region + r * RS + ch * 32);
                 const f32x4 hi = *(const f32x4 *)(region + r * RS + ch * 32 + 16);
@@ -296,6 +297,7 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
             continue;
         }
         // Same-wave LDS accesses complete in order: the rows are readable now.
+        static_assert((32 * CPR) % 64 == 0, "whole lane steps");
 #pragma unroll
         for (int j = 0; j < 32 * CPR / 64; ++j) {
             const int c = lane + 64 * j, r = c / CPR, ch = c % CPR;
@@ -319,19 +321,17 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
 }
 
 // DPP sum over each aligned group of 8 lanes (xor 1, xor 2, half-row mirror).
-// (N = 4: xor 1, xor 2 only.)
-template <int N>
-__device__ __forceinline__ float sum_lanes(float v) {
+__device__ __forceinline__ float sum8_lanes(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    if (N == 8)
-        v += __builtin_bit_cast(float,
-                                __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
     return v;
 }
 
+// amdgpu_waves_per_eu(1): one block of 2–8 waves fills a CU's LDS anyway, so
+// the scheduler may trade occupancy for instruction-level parallelism.
 template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void gemm_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) uint8_t As[2][C::BM * C::ROW];
     __shared__ __attribute__((aligned(16))) uint8_t Bs[2][C::BN * C::ROW];
 
@@ -495,13 +495,15 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::WPE)))
     }
 
     // Row statistics sit past the epilogue staging area of the A buffers.
-    static_assert((C::NT / 64) * 32 * (64 * 4 + 16) + C::BM * 8 <= 2 * C::BM * C::ROW, "epilogue staging exceeds LDS");
+    // Epilogue staging and row statistics reuse the A stages.
+    static_assert((C::NT / 64) * 32 * (C::NTL * 16 * 4 + 16) + C::BM * 8 <= 2 * C::BM * C::ROW,
+                  "epilogue staging exceeds LDS");
     f32x2 *rowstat = (f32x2 *)(&As[0][0] + 2 * C::BM * C::ROW - C::BM * 8);
     if (LNM == fh::LN_IN) {
         const float invk = 1.0f / (float)g.K;
 #pragma unroll
         for (int i = 0; i < C::ACH; ++i) {
-            const float s = sum_lanes<C::CPR>(ssum[i]), q = sum_lanes<C::CPR>(ssq[i]);
+            const float s = sum8_lanes(ssum[i]), q = sum8_lanes(ssq[i]);
             const int rl = (tid + i * C::NT) / C::CPR;
             if ((tid % C::CPR) == 0) {
                 const float mean = s * invk;
@@ -525,10 +527,6 @@ using C1 = Cfg<128, 128, 2, 2, 32, 1>;
 using C2 = Cfg<256, 128, 4, 2, 32, 1>;
 using C3 = Cfg<256, 128, 4, 2, 32, 2>;
 using C5 = Cfg<256, 256, 2, 4, 32, 1>;
-// 4 waves of 128×64 over 64-byte slices: 61 KB of LDS, so two blocks share a
-// CU and one block's epilogue overlaps the other's K loop.
-using C6 = Cfg<256, 128, 2, 2, 16, 1, 64, 2>;
-using C7 = Cfg<256, 128, 2, 2, 16, 2, 64, 2>;
 
 template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
 void launch_one(const GemmArgs &g, hipStream_t s) {
@@ -537,7 +535,9 @@ void launch_one(const GemmArgs &g, hipStream_t s) {
 }
 
 template <class C, bool I8, bool KFULL>
-hipError_t launch_cfg(const GemmArgs &g, int act, bool out_f32, int ln, hipStream_t s) {
+hipError_t launch_cfg(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t s) {
+    GemmArgs g = ga;
+    g.epi_lds = g.epi_lds && g.N % C::BN == 0;  // the staged epilogue writes whole block columns
     if (ln != fh::LN_NONE) {  // binary16 only
         if constexpr (I8) {
             return hipErrorInvalidValue;
@@ -591,7 +591,7 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // statistics need whole 128-byte slices
     if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, ln, s);
     int cfg = forced_cfg();
-    if (cfg < 0 || cfg > 7 || cfg == 4) {
+    if (cfg < 0 || cfg > 5 || cfg == 4) {
         // 256×256 when it still gives every CU a block; 256×128 down to half
         // the CUs (it beats 128×128 on the N = H projections even there).
         const long m256 = (g.M + 255) / 256;
@@ -604,8 +604,6 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, ln, s);
     case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, ln, s);
     case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, ln, s);
-    case 6: return launch_cfg<C6, I8, true>(g, act, out_f32, ln, s);
-    case 7: return launch_cfg<C7, I8, true>(g, act, out_f32, ln, s);
     default: return launch_cfg<C0, I8, true>(g, act, out_f32, ln, s);
     }
 }

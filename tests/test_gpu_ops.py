@@ -53,7 +53,7 @@ def gelu64(x):
 
 
 SHAPES = [(1, 4, 8), (3, 32, 32), (37, 96, 64), (130, 256, 384), (300, 1152, 384), (257, 384, 1536),
-          (129, 132, 40)]
+          (129, 132, 40), (300, 192, 384), (1030, 320, 768)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -73,7 +73,8 @@ def test_gemm_f16_matches_float64(M, N, K):
     np.testing.assert_allclose(got_h, ref - bias, atol=2e-3 * math.sqrt(K) / 8, rtol=1e-3)
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 64, 32), (130, 384, 384), (257, 384, 1536), (300, 768, 768), (129, 132, 40)])
+@pytest.mark.parametrize("M,N,K", [(3, 64, 32), (130, 384, 384), (257, 384, 1536), (300, 768, 768), (129, 132, 40),
+                                   (600, 192, 384), (1030, 320, 768)])
 def test_gemm_f16_residual_rounds_once(M, N, K):
     """Binary16 output with a binary16 residual: bias and residual are added
     in f32 and the sum is rounded once, so the result is within half an f16
