@@ -34,6 +34,11 @@ FLAGS = [
 
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(os.path.dirname(HERE), "include")]
 
+# Per-file code-generation options.  attention.hip: keep MFMA results in
+# VGPRs (its softmax reads every score tile right after the MFMA; in AGPRs
+# each element would cost an extra v_accvgpr_read).
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def sources() -> list[str]:
     hip = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
@@ -46,7 +51,7 @@ def _compile(src: str) -> str:
     if src.endswith(".cpp"):
         cmd = [CXX, *HOST_FLAGS, "-c", src, "-o", obj]
     else:
-        cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+        cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -141,3 +141,24 @@ def _workload_check(name, batch, max_len=None, len_lo=None, threads=16):
 ])
 def test_workload_matches_oracle(name, batch, hi, lo):
     _workload_check(name, batch, hi, lo)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["minilm-l6", "bge-small", "bert-base"])
+def test_gpu_matches_hf_bert_at_real_shapes(name):
+    """The HIP forward against transformers' BertModel (float64) at the real
+    widths, head counts and depths, one ragged batch of the fixture's
+    sequences (tests/golden/bert_shapes.json)."""
+    import json
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "bert_shapes.json")) as f:
+        cases = [c for c in json.load(f)["cases"] if c["workload"] == name]
+    w = synth.workload(name)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    native = _native()
+    m = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    got = m.EncodeBatch([c["ids"] for c in cases])
+    for g, c in zip(got, cases):
+        cos = packio.cosine(g, np.array(c["vector"]))
+        print(f"{name}: L={len(c['ids'])} cos {cos:.7f}")
+        assert cos >= COS_GATE, (name, len(c["ids"]), cos)
+    m.close()

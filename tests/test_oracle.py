@@ -5,7 +5,9 @@ upstream-generated toy goldens (HF BertModel / pinned nomic-bert code), the
 reference's error bounds against float64 libm, its f16 known-answer table,
 the Q8 closed form in int64, and a float64 GEMM.  A deliberately broken
 oracle (a planted mistake) must fail the golden gate."""
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -174,3 +176,29 @@ def test_encode_rejects_like_reference():
     for ids, dim in (([], 0), ([2, 999, 3], 0), ([5] * 65, 0), ([2, 3], 16), ([2, 3], 33)):
         with pytest.raises(ValueError):
             m.encode(ids, dim)
+
+
+def _bert_shape_cases():
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "bert_shapes.json")
+    with open(path) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("workload", ["minilm-l6", "bge-small", "bert-base"])
+def test_oracle_matches_hf_bert_at_real_shapes(workload):
+    """The oracle against transformers' BertModel (float64) on the workload's
+    own synthetic weights at real widths, heads and depths (fixtures written by
+    tests/golden/gen_bert_goldens.py)."""
+    from futon_amd import synth
+    cases = [c for c in _bert_shape_cases() if c["workload"] == workload]
+    assert cases
+    w = synth.workload(workload)
+    t = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    om = oracle.Model(w.config, t)
+    for c in cases:
+        got = om.encode(np.array(c["ids"], dtype=np.int32))
+        want = np.array(c["vector"])
+        cos = float(got @ want / np.linalg.norm(got) / np.linalg.norm(want))
+        assert cos >= 0.999999, (workload, len(c["ids"]), cos)
+        assert np.abs(got - want).max() < 1e-4
+    om.close()
