@@ -107,6 +107,7 @@ struct DevMat {
     void *w = nullptr;       // f16 [n,k] or i8 [n,k]
     float *scale = nullptr;  // i8: [n]
     int n = 0, k = 0;
+    bool ring = false;       // rows stored in fh::ring_pack_row order, multiplied by fh::gemm_ring
 };
 
 struct DevLayer {
@@ -312,10 +313,20 @@ void fold_ln(std::vector<float> &w, int n, int k, const std::vector<float> &g, c
     }
 }
 
-// Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales.
-int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8) {
+// Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales; with
+// ring, as f16 rows in fh::ring_pack_row order for fh::gemm_ring.
+int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8, bool ring = false) {
     d.n = n;
     d.k = k;
+    d.ring = ring && !q8;
+    if (d.ring) {
+        std::vector<uint16_t> h(w.size());
+        for (int r = 0; r < n; r++) {
+            const float *src = &w[(size_t)fh::ring_pack_row(r) * k];
+            for (int j = 0; j < k; j++) h[(size_t)r * k + j] = f32_to_f16(src[j]);
+        }
+        return upload(m, (uint16_t **)&d.w, h.data(), h.size() * 2);
+    }
     if (q8) {
         std::vector<int8_t> codes((size_t)n * k);
         std::vector<float> sc((size_t)n);
@@ -486,7 +497,7 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
                          (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : resid_h ? (double)M * outn * 2 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
+    LCHK(w.ring ? fh::gemm_ring(g, act, out_f32, s) : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
     return FH_OK;
 }
 
@@ -513,7 +524,7 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + (stats_out ? M * 8.0 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(fh::gemm_f16(g, act, false, s, fh::LN_IN));
+    LCHK(w.ring ? fh::gemm_ring(g, act, false, s, fh::LN_IN) : fh::gemm_f16(g, act, false, s, fh::LN_IN));
     return FH_OK;
 }
 
@@ -540,7 +551,7 @@ int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, cons
     const double flops = 2.0 * M * (double)w.n * w.k;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * w.n * 4 + M * 8.0;
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
+    LCHK(w.ring ? fh::gemm_ring(g, fh::ACT_NONE, false, s, fh::RES_LN) : fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
     return FH_OK;
 }
 
@@ -842,6 +853,12 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     const char *fold_env = getenv("FUTON_LN_FOLD");
     m->lnfold = !q8 && H % 64 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16) &&
                 !(fold_env && fold_env[0] == '0');
+    // The folded binary16 projections run on the persistent ring GEMM when
+    // their shape fits it (N % 128, K % 64; not the SwiGLU pair);
+    // FUTON_GEMM_RING=0 keeps them on the tiled GEMM (diagnostics).
+    const char *ring_env = getenv("FUTON_GEMM_RING");
+    const bool ring_on = m->lnfold && !(ring_env && ring_env[0] == '0');
+    auto ring_fits = [&](int n, int k) { return ring_on && n % 128 == 0 && k % 64 == 0; };
     std::vector<float> gA, bA, g1, b1, bias, c1, c2;
     if (m->lnfold && ((rc = ld.vec_host("embeddings.norm.weight", H, gA)) ||
                       (rc = ld.vec_host("embeddings.norm.bias", H, bA))))
@@ -859,9 +876,10 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                 (rc = upload(m, &L.qkv_c2, c2.data(), c2.size() * 4)))
                 return bail(rc);
         }
-        if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8))) return bail(rc);
+        if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8, ring_fits(3 * H, H)))) return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.qkv.bias"), 3 * H, &L.qkv_b, true))) return bail(rc);
-        if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) || (rc = upload_mat(m, L.out, w, H, H, q8)))
+        if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) ||
+            (rc = upload_mat(m, L.out, w, H, H, q8, ring_fits(H, H))))
             return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.out.bias"), H, &L.out_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm1.weight"), H, &L.n1w)) || (rc = ld.vec_f32(nm("norm1.bias"), H, &L.n1b)))
@@ -906,10 +924,13 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                     (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
                     return bail(rc);
             }
+            // FFN1 stays on the tiled GEMM: its 256×256 tiles amortize the
+            // GELU epilogue better than the ring's 256×128 ones.
             if ((rc = upload_mat(m, L.ffn1, w, I, H, q8))) return bail(rc);
             if ((rc = ld.vec_f32(nm("mlp.fc1.bias"), I, &L.ffn1_b, true))) return bail(rc);
         }
-        if ((rc = ld.mat_host(nm("mlp.fc2.weight"), H, I, w)) || (rc = upload_mat(m, L.fc2, w, H, I, q8)))
+        if ((rc = ld.mat_host(nm("mlp.fc2.weight"), H, I, w)) ||
+            (rc = upload_mat(m, L.fc2, w, H, I, q8, ring_fits(H, I))))
             return bail(rc);
         if ((rc = ld.vec_f32(nm("mlp.fc2.bias"), H, &L.fc2_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm2.weight"), H, &L.n2w)) || (rc = ld.vec_f32(nm("norm2.bias"), H, &L.n2b)))

@@ -10,6 +10,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // 64-lane wavefront helpers (CDNA).
@@ -71,6 +72,18 @@ enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_RES16 = 3 };
 enum LnMode { LN_NONE = 0, LN_IN = 1, RES_LN = 2 };
 hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);
 hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
+// Persistent LDS-ring GEMM (gemm_ring.hip).  B must be packed with
+// ring_pack_row (rows permuted inside each 64-row block); gemm_ring_ok says
+// whether a problem fits it (binary16, N % 128 == 0, K % 64 == 0, no SwiGLU).
+bool gemm_ring_ok(const GemmArgs &a, int act, bool out_f32, int ln);
+hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);
+// out = B with rows in ring_pack_row order (N % 64 == 0, K % 8 == 0).
+hipError_t ring_pack(const f16 *B, f16 *out, int N, int K, hipStream_t s);
+// Row of the unpacked weight matrix stored at packed row r.
+__host__ __device__ inline int ring_pack_row(int r) {
+    const int p = r & 63, tn = p >> 4, g = (p >> 2) & 3, e = p & 3;
+    return (r & ~63) | ((tn >> 1) * 32 + g * 8 + (tn & 1) * 4 + e);
+}
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
 // gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
 // binary16 sum to x16 instead, for a consumer that folds this LayerNorm.

@@ -40,6 +40,81 @@ extern "C" int fh_op_gemm(int32_t dtype, const void *A, const void *B, const flo
     return code_of(dtype == FH_OP_I8 ? fh::gemm_i8(g, act, out_f32 != 0, s) : fh::gemm_f16(g, act, out_f32 != 0, s));
 }
 
+extern "C" int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, const void *resid,
+                               int32_t resid_f16, void *C, int32_t M, int32_t N, int32_t K, int32_t act,
+                               int32_t out_f32, void *stream) {
+    if (!A || !B_packed || !C || M < 0 || N <= 0 || K <= 0) return FH_EINVAL;
+    if (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU) return FH_EINVAL;
+    if (resid && resid_f16 && (out_f32 || act != FH_OP_ACT_NONE)) return FH_EINVAL;
+    if (M == 0) return FH_OK;
+    GemmArgs g{};
+    g.A = A;
+    g.B = B_packed;
+    g.bias = bias;
+    g.resid = resid_f16 ? nullptr : (const float *)resid;
+    g.resid_h = resid_f16 ? (const f16 *)resid : nullptr;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = K;
+    g.ldb = K;
+    g.ldc = N;
+    g.ldr = N;
+    const int a = act == FH_OP_ACT_NONE && !out_f32 && g.resid_h ? fh::ACT_RES16 : act;
+    if (!fh::gemm_ring_ok(g, a, out_f32 != 0, fh::LN_NONE)) return FH_EINVAL;
+    return code_of(fh::gemm_ring(g, act, out_f32 != 0, (hipStream_t)stream));
+}
+
+extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const void *B, const float *c1,
+                             const float *c2, void *stats_out, float eps, const float *bias, const void *resid_h,
+                             const void *stats_in, const float *ln_g, const float *ln_b, void *C, int32_t M,
+                             int32_t N, int32_t K, int32_t act, void *stream) {
+    if (!A || !B || !C || M < 0 || N <= 0 || K <= 0 || K % 64 || N % 4) return FH_EINVAL;
+    GemmArgs g{};
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = K;
+    g.ldb = K;
+    g.ldc = N;
+    g.ldr = N;
+    int a;
+    if (ln_mode == fh::LN_IN) {
+        if (!c1 || !c2 || (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU)) return FH_EINVAL;
+        g.c1 = c1;
+        g.c2 = c2;
+        g.stats_out = (f32x2 *)stats_out;
+        g.ln_eps = eps;
+        a = act;
+    } else if (ln_mode == fh::RES_LN) {
+        if (!resid_h || !stats_in || !ln_g || !ln_b || act != FH_OP_ACT_NONE) return FH_EINVAL;
+        g.bias = bias;
+        g.resid_h = (const f16 *)resid_h;
+        g.stats_in = (const f32x2 *)stats_in;
+        g.ln_g = ln_g;
+        g.ln_b = ln_b;
+        a = fh::ACT_RES16;
+    } else {
+        return FH_EINVAL;
+    }
+    if (M == 0) return FH_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (ring) {
+        if (!fh::gemm_ring_ok(g, a, false, ln_mode)) return FH_EINVAL;
+        return code_of(fh::gemm_ring(g, a, false, s, ln_mode));
+    }
+    return code_of(fh::gemm_f16(g, ln_mode == fh::RES_LN ? (int)fh::ACT_NONE : a, false, s, ln_mode));
+}
+
+extern "C" int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream) {
+    if (!B || !out || N <= 0 || K <= 0 || N % 64 || K % 8) return FH_EINVAL;
+    return code_of(fh::ring_pack((const f16 *)B, (f16 *)out, N, K, (hipStream_t)stream));
+}
+
 extern "C" int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32_t max_len, int32_t H,
                                int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
                                int32_t q_limit, int32_t compact, int32_t out_f32, void *stream) {

@@ -20,8 +20,10 @@
 #include <cstdlib>
 
 #include "fh_common.h"
+#include "gemm_epi.h"
 
 namespace {
+using namespace fh_epi;
 
 constexpr int KFULL_BYTES = 128;  // K (in bytes) multiple every full-slice configuration divides
 
@@ -40,24 +42,6 @@ struct Cfg {
     static constexpr int BCH = BN * CPR / NT;
     static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/thread mismatch");
 };
-
-// erf-GELU, 0.5·x·(1 + erf(x/√2)) (native/mathf32.go:96-107), with the
-// hardware reciprocal and exp.
-__device__ __forceinline__ float gelu_erf(float x) {
-    // x·Φ(x) with erfc(z) = t·P(t)·exp(−z²), t = 1/(1 + p·z), z = |x|/√2
-    // (Abramowitz & Stegun 7.1.26, |error| ≤ 1.5e-7).  Constants folded:
-    // p/√2, ½·a_i, and exp(−x²/2) = 2^(−x²·½·log2 e).
-    const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.23164190f, 1.0f));
-    float q = 0.53070271f;
-    q = fmaf(q, t, -0.72657601f);
-    q = fmaf(q, t, 0.71070687f);
-    q = fmaf(q, t, -0.14224837f);
-    q = fmaf(q, t, 0.12741480f);
-    const float e = __builtin_amdgcn_exp2f((x * x) * -0.72134752f);
-    const float h = x * (q * t) * e;  // ½·x·erfc(|x|/√2)
-    return x < 0.f ? h : x - h;
-}
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences
 // global memory, which makes every barrier wait for all in-flight global
@@ -80,23 +64,6 @@ __device__ __forceinline__ void tile_coords(int &mt, int &nt) {
     nt = logical - mt * gx;
 }
 
-// LN_IN fold of one 4-column group: rstd·(acc − mean·c1) + c2.
-__device__ __forceinline__ f32x4 ln_fold(const GemmArgs &g, int col, f32x4 v, f32x2 rs) {
-    const f32x4 c1 = *(const f32x4 *)(g.c1 + col), c2 = *(const f32x4 *)(g.c2 + col);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rs[1] * (v[i] - rs[0] * c1[i]) + c2[i];
-    return v;
-}
-// RES_LN residual of 4 columns: (y − mean)·rstd·γ + β.
-__device__ __forceinline__ f32x4 ln_resid(const GemmArgs &g, int row, int col, f16x4 y) {
-    const f32x2 st = g.stats_in[row];
-    const f32x4 gm = *(const f32x4 *)(g.ln_g + col), bt = *(const f32x4 *)(g.ln_b + col);
-    f32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = ((float)y[i] - st[0]) * st[1] * gm[i] + bt[i];
-    return r;
-}
-
 template <int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int col, f32x4 v,
                                                f32x4 gate, f32x2 rs) {
@@ -117,7 +84,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
         if (OUT_F32) {
             *(f32x4 *)((float *)g.C + (size_t)row * g.ldc + ocol) = o;
         } else {
-            f16x4 h = {(f16)o[0], (f16)o[1], (f16)o[2], (f16)o[3]};
+            f16x4 h = {to_f16(o[0]), to_f16(o[1]), to_f16(o[2]), to_f16(o[3])};
             *(f16x4 *)((f16 *)g.C + (size_t)row * g.ldc + ocol) = h;
         }
         return;
@@ -137,7 +104,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
     if (OUT_F32) {
         *(f32x4 *)((float *)g.C + (size_t)row * g.ldc + col) = v;
     } else {
-        f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        f16x4 h = {to_f16(v[0]), to_f16(v[1]), to_f16(v[2]), to_f16(v[3])};
         *(f16x4 *)((f16 *)g.C + (size_t)row * g.ldc + col) = h;
     }
 }
@@ -254,7 +221,7 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 if (OUT_F32 || R16) {
                     *(f32x4 *)dst = v;
                 } else {
-                    *(f16x4 *)dst = (f16x4){(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                    *(f16x4 *)dst = (f16x4){to_f16(v[0]), to_f16(v[1]), to_f16(v[2]), to_f16(v[3])};
                 }
             }
         }
@@ -289,8 +256,8 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 f16x8 o;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    o[i] = (f16)(lo[i] + r0[i]);
-                    o[4 + i] = (f16)(hi[i] + r1[i]);
+                    o[i] = to_f16(lo[i] + r0[i]);
+                    o[4 + i] = to_f16(hi[i] + r1[i]);
                 }
                 *(f16x8 *)((f16 *)g.C + (size_t)grow * g.ldc + gcol) = o;
             }
@@ -506,9 +473,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
             const float s = sum8_lanes(ssum[i]), q = sum8_lanes(ssq[i]);
             const int rl = (tid + i * C::NT) / C::CPR;
             if ((tid % C::CPR) == 0) {
-                const float mean = s * invk;
-                const float var = fmaxf(q * invk - mean * mean, 0.f);
-                const f32x2 st = {mean, 1.0f / sqrtf(var + g.ln_eps)};
+                const f32x2 st = ln_stats(s, q, invk, g.ln_eps);
                 rowstat[rl] = st;
                 if (g.stats_out && nt == 0 && m0 + rl < g.M) g.stats_out[m0 + rl] = st;
             }

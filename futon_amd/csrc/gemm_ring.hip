@@ -1,0 +1,417 @@
+// Persistent binary16 GEMM for the encoder's projections on gfx950:
+// C[M,N] = A[M,K] · Bᵀ, the contraction of the reference's Kernel.MatMulTF16
+// (native/kernel.go:26-43) with the same epilogues as gemm.hip (bias, GELU,
+// residual, the folded-LayerNorm modes).
+//
+// Layout and schedule:
+// * One 512-thread block per CU, looping over 256×128 output tiles; each of
+//   the 8 XCDs owns a contiguous range of tiles, so an A row panel is fetched
+//   into one XCD's L2 and reused there by all of that panel's column tiles.
+// * Operands stream into a 3-slot LDS ring (48 KB per 64-wide K slice)
+//   straight from global memory with buffer_load … lds (no VGPR staging, no
+//   LDS store instructions).  The ring runs across tile boundaries: the next
+//   tile's first slices are in flight during the current tile's last slice
+//   and its epilogue.  Rows past M read as zero through the buffer range
+//   check.
+// * LDS rows are 128 bytes with the 16-byte chunk index XOR-ed with row%8,
+//   which makes the MFMA fragment reads (16 rows × one chunk) conflict-free.
+// * v_mfma_f32_16x16x32_f16 with the weight fragment as the A operand: a
+//   lane holds four consecutive MFMA rows of one token.  The weights are
+//   stored permuted within each 64-row block (ring_pack_row) so that those
+//   MFMA rows are output features g·8 + {0..7} (+32), and every lane writes
+//   two whole 16-byte runs of 8 features: coalesced stores straight from
+//   registers, no LDS staging.
+// The accumulation order over K is the one gemm.hip uses (same slices, same
+// MFMA shape, same LN statistics reduction), so both kernels give the same
+// bits for the same operands.
+#include <cstdlib>
+
+#include "fh_common.h"
+#include "gemm_epi.h"
+
+namespace {
+using namespace fh_epi;
+
+constexpr int BM = 256, BN = 128, WM = 4, WN = 2, SLOTS = 3;
+constexpr int NT = 64 * WM * WN;                  // 512 threads
+constexpr int MT = BM / WM / 16;                  // token tiles per wave (4)
+constexpr int NTL = BN / WN / 16;                 // feature tiles per wave (4: the 64-row packing block)
+constexpr int ROWB = 128;                         // bytes of K per slice row (64 f16)
+constexpr int STAGE = (BM + BN) * ROWB;           // bytes per ring slot
+constexpr int DPW = (BM + BN) / 8 / (WM * WN);    // 1-KB DMA blocks per wave per slice
+static_assert(NTL == 4 && DPW * 8 * WM * WN == BM + BN && BM % 8 == 0, "tile shape");
+
+// Buffer resource for raw 16-byte loads of `bytes` bytes at p: offsets at or
+// beyond `bytes` read as zero.
+__device__ __forceinline__ i32x4 buf_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return (i32x4){(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
+// 16 bytes per lane from rs + voff + soff into LDS at lds_addr + lane·16.
+// Issued as inline assembly: the compiler does not track LDS written by the
+// DMA path, so the ring's waits are explicit (s_waitcnt vmcnt + barrier).
+__device__ __forceinline__ void dma16(i32x4 rs, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(rs), "s"(soff)
+                 : "memory", "m0");
+}
+
+// RES: no residual (0), f32 (1) or binary16 (2); BIAS: g.bias is set.  The
+// epilogue is straight-line code for each combination, so the number of
+// vector memory instructions it issues is a constant the ring's waits use.
+template <int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ring_kernel(GemmArgs g, int ntn,
+                                                                                           int per_xcd) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[SLOTS * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    // This block's tiles: XCD x (= block id mod 8) owns tiles
+    // [x·per_xcd, (x+1)·per_xcd); its blocks take them round-robin.
+    const int ntiles = ((g.M + BM - 1) / BM) * ntn;
+    const int nbx = gridDim.x >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int t0 = xcd * per_xcd + j, tend = min(ntiles, (xcd + 1) * per_xcd);
+    const int ntile = t0 < tend ? (tend - t0 + nbx - 1) / nbx : 0;
+    const int nk = g.K / 64;
+    const int nsl = ntile * nk;  // slices this block multiplies
+    if (nsl == 0) return;
+
+    const uint32_t lda_b = (uint32_t)g.lda * 2, ldb_b = (uint32_t)g.ldb * 2;
+    const i32x4 rA = buf_rsrc(g.A, (uint32_t)g.M * lda_b);
+    const i32x4 rB = buf_rsrc(g.B, (uint32_t)g.N * ldb_b);
+    const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
+
+    // DMA block b of a slot holds slot rows 8b..8b+7 (rows < BM: A, else B);
+    // lane l writes physical chunk l%8 of row 8b + l/8, i.e. logical chunk
+    // (l%8) ^ (l/8).
+    const uint32_t lrow = lane >> 3, lchunk = ((lane & 7) ^ (lane >> 3)) * 16;
+    // Per DMA block of this wave (wave-uniform, fixed for the kernel): operand
+    // and row offset inside the tile's operand rows.
+    bool isA[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) isA[i] = (wave * DPW + i) * 8 < BM;
+    // Issues slice s of this block's sequence (past the end: the last slice
+    // again, into a slot nobody reads) into slot s % SLOTS.
+    auto issue = [&](int s) {
+        const int sc = min(s, nsl - 1);
+        const int ti = sc / nk, kk = sc - ti * nk;
+        const int t = t0 + ti * nbx;
+        const int mt = t / ntn, nt = t - mt * ntn;
+        const uint32_t slot = ring0 + (uint32_t)(s % SLOTS) * STAGE;
+        const uint32_t soff = (uint32_t)kk * ROWB;
+        const uint32_t offA = (uint32_t)(mt * BM) * lda_b + lrow * lda_b + lchunk;
+        const uint32_t offB = (uint32_t)(nt * BN - BM) * ldb_b + lrow * ldb_b + lchunk;
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) {
+            const uint32_t b = (uint32_t)(wave * DPW + i);
+            const uint32_t dst = slot + b * 1024;
+            const uint32_t voff = isA[i] ? offA + b * 8 * lda_b : offB + b * 8 * ldb_b;
+            dma16(isA[i] ? rA : rB, dst, voff, soff);
+        }
+    };
+
+    // Fragment offsets inside a slot: row r = base + lane%16 (base a multiple
+    // of 16), logical chunk lane/16 + 4·ks at physical chunk ^ (lane%8).
+    int fo[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) fo[ks] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * ks) ^ (lane & 7)) << 4);
+    const int abase = wm * MT * 16 * ROWB, bbase = BM * ROWB + wn * NTL * 16 * ROWB;
+
+    f32x4 acc[NTL][MT];
+    float ssum[2][MT], ssq[2][MT];  // LN_IN: per chunk-of-8 partial sums of this lane's rows
+    auto clear = [&] {
+#pragma unroll
+        for (int a = 0; a < NTL; ++a)
+#pragma unroll
+            for (int b = 0; b < MT; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int b = 0; b < MT; ++b) ssum[ks][b] = ssq[ks][b] = 0.f;
+    };
+    clear();
+
+    auto compute = [&](int slot) {
+        const uint8_t *base = ring + slot * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            i32x4 af[MT], bf[NTL];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(base + abase + t * 16 * ROWB + fo[ks]);
+#pragma unroll
+            for (int t = 0; t < NTL; ++t) bf[t] = *(const i32x4 *)(base + bbase + t * 16 * ROWB + fo[ks]);
+            if (LNM == fh::LN_IN) {
+                const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const f16x8 h = __builtin_bit_cast(f16x8, af[t]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f16x2 pr = {h[2 * q], h[2 * q + 1]};
+                        ssum[ks][t] = __builtin_amdgcn_fdot2(pr, one, ssum[ks][t], false);
+                        ssq[ks][t] = __builtin_amdgcn_fdot2(pr, pr, ssq[ks][t], false);
+                    }
+                }
+            }
+#pragma unroll
+            for (int tn = 0; tn < NTL; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < MT; ++tm)
+                    acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[tm]), acc[tn][tm], 0, 0, 0);
+        }
+    };
+
+    // Epilogue of tile ti, in two parts.  epi_load issues the loads the
+    // epilogue needs (column constants, binary16 residual rows, statistics)
+    // before the ring's DMA of the tile's last slice: a wait for a load queued
+    // behind those DMAs would also wait for them.  epi_store does the
+    // arithmetic, gemm.hip's epilogue_store term for term, and the stores:
+    // buffer stores, whose range check drops rows past M, so every lane of
+    // every wave issues exactly NSTORE of them.
+    // This lane's 16 features: cb + 32·h + 4·half + {0..3}, q = 2·h + half.
+    constexpr int ESZ = OUT_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t rC =
+        __builtin_amdgcn_make_buffer_rsrc(g.C, (short)0, (int)((uint32_t)g.M * (uint32_t)g.ldc * ESZ), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
+        g.stats_out ? (void *)g.stats_out : g.C, (short)0, g.stats_out ? g.M * 8 : 0, 0x00020000);
+    f32x4 k1[4], k2[4], kb[4], kg[4], kt[4];
+    f16x8 rh[MT][2];
+    f32x2 sti[MT];
+    auto tile_of = [&](int ti, int &m0, int &nt) {
+        const int t = t0 + ti * nbx;
+        const int mt = t / ntn;
+        nt = t - mt * ntn;
+        m0 = mt * BM;
+    };
+    auto epi_load = [&](int ti) {
+        int m0, nt;
+        tile_of(ti, m0, nt);
+        const int cb = nt * BN + wn * NTL * 16 + (lane >> 4) * 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int col = cb + (q >> 1) * 32 + (q & 1) * 4;
+            if (LNM == fh::LN_IN) {
+                k1[q] = *(const f32x4 *)(g.c1 + col);
+                k2[q] = *(const f32x4 *)(g.c2 + col);
+            }
+            if (BIAS) kb[q] = *(const f32x4 *)(g.bias + col);
+            if (LNM == fh::RES_LN) {
+                kg[q] = *(const f32x4 *)(g.ln_g + col);
+                kt[q] = *(const f32x4 *)(g.ln_b + col);
+            }
+        }
+        // Rows past M are clamped to M−1: loaded, never stored.
+#pragma unroll
+        for (int tm = 0; tm < MT; ++tm) {
+            const int rr = min(m0 + (wm * MT + tm) * 16 + (lane & 15), g.M - 1);
+            if (RES == 2) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) rh[tm][h] = *(const f16x8 *)(g.resid_h + (size_t)rr * g.ldr + cb + h * 32);
+            }
+            if (LNM == fh::RES_LN) sti[tm] = g.stats_in[rr];
+        }
+    };
+    auto epi_store = [&](int ti) {
+        int m0, nt;
+        tile_of(ti, m0, nt);
+        const int cb = nt * BN + wn * NTL * 16 + (lane >> 4) * 8;
+        // An f32 residual (too many registers to hold across the last slice)
+        // is loaded here, still ahead of the stores.
+        f32x4 rf[MT][4];
+        if (RES == 1) {
+#pragma unroll
+            for (int tm = 0; tm < MT; ++tm) {
+                const int rr = min(m0 + (wm * MT + tm) * 16 + (lane & 15), g.M - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    rf[tm][q] = *(const f32x4 *)(g.resid + (size_t)rr * g.ldr + cb + (q >> 1) * 32 + (q & 1) * 4);
+            }
+        }
+#pragma unroll
+        for (int tm = 0; tm < MT; ++tm) {
+            const uint32_t row = (uint32_t)(m0 + (wm * MT + tm) * 16 + (lane & 15));
+            f32x2 rs = {0.f, 0.f};
+            if (LNM == fh::LN_IN) {
+                // Chunk sums c0..c7 of the row sit in lane groups 0..3 (ks 0:
+                // chunk g, ks 1: chunk g+4); reduce as ((c0+c1)+(c2+c3)) +
+                // ((c4+c5)+(c6+c7)), gemm.hip's order.
+                float s0 = ssum[0][tm], s1 = ssum[1][tm], q0 = ssq[0][tm], q1 = ssq[1][tm];
+                s0 += __shfl_xor(s0, 16, 64);
+                s1 += __shfl_xor(s1, 16, 64);
+                q0 += __shfl_xor(q0, 16, 64);
+                q1 += __shfl_xor(q1, 16, 64);
+                s0 += __shfl_xor(s0, 32, 64);
+                s1 += __shfl_xor(s1, 32, 64);
+                q0 += __shfl_xor(q0, 32, 64);
+                q1 += __shfl_xor(q1, 32, 64);
+                const float invk = 1.0f / (float)g.K;
+                rs = ln_stats(s0 + s1, q0 + q1, invk, g.ln_eps);
+                // One lane per row of the first column tile writes it; the
+                // others aim past the buffer's range.
+                const bool w = nt == 0 && wn == 0 && lane < 16;
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, rs), rS, w ? row * 8u : 0xfffffff0u, 0,
+                                                      0);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                f32x4 v[2];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int q = 2 * h + half;
+                    f32x4 x = acc[q][tm];
+                    if (LNM == fh::LN_IN) x = ln_fold_v(x, rs, k1[q], k2[q]);
+                    if (BIAS) x += kb[q];
+                    if (ACT == fh::ACT_GELU) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) x[i] = gelu_erf(x[i]);
+                    }
+                    if (RES == 1) {
+                        x += rf[tm][q];
+                    } else if (RES == 2) {
+                        const f16x8 r8 = rh[tm][h];
+                        const f16x4 r4 = half ? (f16x4){r8[4], r8[5], r8[6], r8[7]} : (f16x4){r8[0], r8[1], r8[2], r8[3]};
+                        if (LNM == fh::RES_LN) x += ln_resid_v(r4, sti[tm], kg[q], kt[q]);
+                        else x += (f32x4){(float)r4[0], (float)r4[1], (float)r4[2], (float)r4[3]};
+                    }
+                    v[half] = x;
+                }
+                const uint32_t off = (row * (uint32_t)g.ldc + (uint32_t)(cb + h * 32)) * ESZ;
+                if (OUT_F32) {
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v[0]), rC, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v[1]), rC, off + 16, 0, 0);
+                } else {
+                    f16x8 o;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        o[i] = to_f16(v[0][i]);
+                        o[4 + i] = to_f16(v[1][i]);
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), rC, off, 0, 0);
+                }
+            }
+        }
+    };
+    // Vector memory instructions epi_store issues after its loads.
+    constexpr int NSTORE = MT * (OUT_F32 ? 4 : 2) + (LNM == fh::LN_IN ? MT : 0);
+
+    // Ring: slice s lives in slot s % 3; two slices are in flight while one
+    // is multiplied.  Before multiplying slice s this wave waits until slice
+    // s's DMA has landed, then the barrier makes every wave's part of slice s
+    // visible and frees the slot slice s-1 used, for slice s+2.  Vector memory
+    // operations retire in order, so "slice s landed" is "at most n younger
+    // operations outstanding".  Issued after slice s's DMA: slice s+1's DMA
+    // (DPW), and the NSTORE stores of an epilogue that ended slice s−1 or
+    // s−2 (its loads have been consumed, so they are not outstanding).
+    // Counting more than were issued would not wait long enough: n counts at
+    // most one epilogue.
+    issue(0);
+    issue(1);
+    for (int s = 0; s < nsl; ++s) {
+        const int ks = s % nk;
+        if (s >= 1 && (ks == 0 || (ks == 1 && s >= 2))) {
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPW + NSTORE) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPW) : "memory");
+        }
+        const bool tile_end = (s + 1) % nk == 0;
+        if (tile_end) epi_load(s / nk);
+        issue(s + 2);
+        compute(s % SLOTS);
+        if (tile_end) {
+            epi_store(s / nk);
+            clear();
+        }
+    }
+    // The DMA path writes this block's LDS: drain it before the block ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return hipErrorUnknown;
+        ncu = p.multiProcessorCount;
+    }
+    const int ntn = g.N / BN;
+    const long ntiles = (long)((g.M + BM - 1) / BM) * ntn;
+    // A multiple of 8 blocks (whole XCD groups), at most one per CU.
+    const int cap = (ncu / 8) * 8;
+    const int grid = (int)std::min<long>(cap, (ntiles + 7) / 8 * 8);
+    const int per_xcd = (int)((ntiles + 7) / 8);
+    hipLaunchKernelGGL((ring_kernel<ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(NT), 0, s, g, ntn, per_xcd);
+    return hipGetLastError();
+}
+
+// Selects the kernel for g's bias and residual pointers.
+template <int ACT, bool OUT_F32, int LNM>
+hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+    const int res = g.resid ? 1 : g.resid_h ? 2 : 0;
+    if (ACT == fh::ACT_RES16 || LNM == fh::RES_LN) {  // binary16 residual by construction
+        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 2>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 2>(g, s);
+    }
+    if (LNM == fh::LN_IN || res == 0) {
+        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 0>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 0>(g, s);
+    }
+    if (res == 1) {
+        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 1>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 1>(g, s);
+    }
+    return hipErrorInvalidValue;  // a binary16 residual outside ACT_RES16
+}
+
+// out row r ← B row ring_pack_row(r), 16 bytes per thread.
+__global__ void ring_pack_kernel(const f16 *__restrict__ B, f16 *__restrict__ out, int N, int K) {
+    const long c = (long)blockIdx.x * blockDim.x + threadIdx.x, cpr = K / 8;
+    if (c >= (long)N * cpr) return;
+    const int r = (int)(c / cpr), ch = (int)(c - (long)r * cpr);
+    *(f16x8 *)(out + (size_t)r * K + ch * 8) = *(const f16x8 *)(B + (size_t)fh::ring_pack_row(r) * K + ch * 8);
+}
+
+}  // namespace
+
+namespace fh {
+
+hipError_t ring_pack(const f16 *B, f16 *out, int N, int K, hipStream_t s) {
+    if (N % 64 || K % 8 || N <= 0 || K <= 0) return hipErrorInvalidValue;
+    const long n = (long)N * (K / 8);
+    hipLaunchKernelGGL(ring_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, B, out, N, K);
+    return hipGetLastError();
+}
+
+bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
+    if (g.M <= 0 || g.N % BN != 0 || g.K % 64 != 0 || g.K <= 0) return false;
+    if (act != ACT_NONE && act != ACT_GELU && act != ACT_RES16) return false;
+    if (g.lda % 8 || g.ldb % 8 || g.ldc % 8 || ((g.resid || g.resid_h) && g.ldr % 8)) return false;
+    if (act == ACT_RES16 && (out_f32 || !g.resid_h)) return false;
+    if (ln == LN_IN && (out_f32 || g.resid || g.resid_h)) return false;
+    if (act != ACT_RES16 && ln != RES_LN && g.resid_h && !g.resid) return false;
+    if (ln == RES_LN && (out_f32 || !g.resid_h || g.resid)) return false;
+    // 32-bit buffer offsets: every row the ring addresses (up to M + BM − 1).
+    if (((double)g.M + BM) * g.lda * 2.0 >= 2147483648.0 || (double)g.N * g.ldb * 2.0 >= 2147483648.0) return false;
+    if (((double)g.M + BM) * g.ldc * (out_f32 ? 4.0 : 2.0) >= 2147483648.0) return false;
+    return true;
+}
+
+hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln) {
+    if (act == ACT_NONE && !out_f32 && a.resid_h && !a.resid) act = ACT_RES16;
+    if (!gemm_ring_ok(a, act, out_f32, ln)) return hipErrorInvalidValue;
+    if (ln == LN_IN) {
+        if (act == ACT_NONE) return launch_ring<ACT_NONE, false, LN_IN>(a, s);
+        if (act == ACT_GELU) return launch_ring<ACT_GELU, false, LN_IN>(a, s);
+        return hipErrorInvalidValue;
+    }
+    if (ln == RES_LN) return launch_ring<ACT_RES16, false, RES_LN>(a, s);
+    if (act == ACT_RES16) return launch_ring<ACT_RES16, false, LN_NONE>(a, s);
+    if (act == ACT_GELU)
+        return out_f32 ? launch_ring<ACT_GELU, true, LN_NONE>(a, s) : launch_ring<ACT_GELU, false, LN_NONE>(a, s);
+    return out_f32 ? launch_ring<ACT_NONE, true, LN_NONE>(a, s) : launch_ring<ACT_NONE, false, LN_NONE>(a, s);
+}
+
+}  // namespace fh

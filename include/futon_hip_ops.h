@@ -35,6 +35,34 @@ int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, c
                int32_t resid_f16, const float *a_scale, const float *b_scale, void *C, int32_t M, int32_t N,
                int32_t K, int32_t act, int32_t out_f32, void *stream);
 
+/* The same contraction on the persistent LDS-ring kernel (binary16 only):
+ * B_packed is B with its rows permuted by fh_op_ring_pack.  Requires
+ * N % 128 == 0 and K % 64 == 0; act is NONE or GELU.  Gives the same bits
+ * as fh_op_gemm on the unpacked B.
+ * Replaces: Kernel.MatMulTF16 (native/kernel.go:26-43). */
+int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, const void *resid, int32_t resid_f16,
+                    void *C, int32_t M, int32_t N, int32_t K, int32_t act, int32_t out_f32, void *stream);
+
+/* The folded-LayerNorm forms of the binary16 GEMM (K % 64 == 0), on the
+ * tiled kernel (ring = 0, B as is) or the ring kernel (ring = 1, B packed):
+ *  ln_mode 1 (LN_IN):  C = act(rstd·(A·Bᵀ − mean·c1) + c2), (mean, rstd) of
+ *                      A's rows (eps) to stats_out [M] float pairs if set;
+ *                      act NONE or GELU.
+ *  ln_mode 2 (RES_LN): C = A·Bᵀ + bias + (resid_h − mean)·rstd·ln_g + ln_b
+ *                      with (mean, rstd) from stats_in, rounded once.
+ * C is binary16 [M, N].  These are the model's LayerNorm folds of
+ * native/model.go:555-633 (LN(x)·Wᵀ and the residual LN). */
+int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const void *B, const float *c1, const float *c2,
+                  void *stats_out, float eps, const float *bias, const void *resid_h, const void *stats_in,
+                  const float *ln_g, const float *ln_b, void *C, int32_t M, int32_t N, int32_t K, int32_t act,
+                  void *stream);
+
+/* Row permutation of a binary16 [N, K] weight matrix (N % 64 == 0, K % 8 == 0)
+ * into the order fh_op_gemm_ring reads: inside each 64-row block, packed row
+ * 16·t + 4·g + e holds row 32·(t/2) + 8·g + 4·(t%2) + e.  No reference
+ * counterpart (a layout of this build). */
+int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream);
+
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,
  * holding each sequence's first q_limit=1 query row), f32 or binary16.

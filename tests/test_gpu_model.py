@@ -162,3 +162,24 @@ def test_gpu_matches_hf_bert_at_real_shapes(name):
         print(f"{name}: L={len(c['ids'])} cos {cos:.7f}")
         assert cos >= COS_GATE, (name, len(c["ids"]), cos)
     m.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,batch", [("minilm-l6", 8), ("bge-small", 24), ("bert-base", 3)])
+def test_ring_gemm_forward_equals_tiled(name, batch, monkeypatch):
+    """The folded binary16 forward returns the same bits whether its
+    projections run on the persistent ring GEMM (the default) or on the tiled
+    GEMM (FUTON_GEMM_RING=0): same K order, same LayerNorm statistics
+    reduction, same epilogue arithmetic."""
+    w = synth.workload(name)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    ids, offsets = synth.make_batch(w.ids_seed + 7, batch, w.len_lo, w.len_hi)
+    native = _native()
+    ring = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    monkeypatch.setenv("FUTON_GEMM_RING", "0")
+    tiled = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    a = ring.EncodePacked(ids, offsets, w.out_dim)
+    b = tiled.EncodePacked(ids, offsets, w.out_dim)
+    assert np.array_equal(a, b), np.abs(a - b).max()
+    ring.close()
+    tiled.close()

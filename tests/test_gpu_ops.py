@@ -90,6 +90,131 @@ def test_gemm_f16_residual_rounds_once(M, N, K):
     assert np.all(np.abs(got - ref) <= 0.5 * ulp + 2e-5 * math.sqrt(K)), np.abs(got - ref).max()
 
 
+def ring_perm(N):
+    """Packed row 16·t + 4·g + e of each 64-row block holds row
+    32·(t//2) + 8·g + 4·(t%2) + e (include/futon_hip_ops.h)."""
+    p = np.empty(N, np.int64)
+    for r in range(N):
+        q = r % 64
+        t, g, e = q // 16, (q // 4) % 4, q % 4
+        p[r] = r - q + 32 * (t // 2) + 8 * g + 4 * (t % 2) + e
+    return p
+
+
+def gemm_ring(A, Bp, bias=None, resid=None, act=0, out_f32=True):
+    M, K = A.shape
+    N = Bp.shape[0]
+    C = torch.empty((M, N), dtype=torch.float32 if out_f32 else torch.float16, device="cuda")
+    resid_f16 = int(resid is not None and resid.dtype == torch.float16)
+    rc = _lib().fh_op_gemm_ring(ptr(A), ptr(Bp), ptr(bias), ptr(resid), resid_f16, ptr(C), M, N, K, act,
+                                int(out_f32), None)
+    assert rc == 0
+    sync()
+    return C.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (77, 128, 64), (300, 384, 384), (513, 1152, 384),
+                                   (1030, 1536, 384), (257, 384, 1536), (2049, 768, 768), (18048, 384, 384)])
+def test_gemm_ring_equals_tiled(M, N, K):
+    """The persistent LDS-ring GEMM on packed weights returns fh_op_gemm's
+    bits on the unpacked weights (same K order, same epilogue arithmetic),
+    for f32 and binary16 outputs with bias, GELU and f32 / binary16
+    residuals; ragged M exercises the zero rows past the end."""
+    rng = np.random.default_rng(M * 5 + N + K)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    b = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    r32 = rng.standard_normal((M, N)).astype(np.float32)
+    r16 = (rng.standard_normal((M, N)) * 2).astype(np.float16)
+    da, db, dbias, d32, d16 = dev(a), dev(b), dev(bias), dev(r32), dev(r16)
+    bp = torch.empty_like(db)
+    assert _lib().fh_op_ring_pack(ptr(db), ptr(bp), N, K, None) == 0
+    sync()
+    assert np.array_equal(bp.cpu().numpy(), b[ring_perm(N)])
+    cases = [dict(bias=dbias, resid=d32), dict(bias=dbias, act=1), dict(out_f32=False),
+             dict(bias=dbias, resid=d16, out_f32=False), dict(bias=dbias, act=1, out_f32=False)]
+    for kw in cases:
+        want = gemm(0, da, db, **kw)
+        got = gemm_ring(da, bp, **kw)
+        assert np.array_equal(got, want), (kw.keys(), np.abs(got.astype(np.float64) - want).max())
+    ref = a.astype(np.float64) @ b.astype(np.float64).T + bias
+    np.testing.assert_allclose(gemm_ring(da, bp, dbias), ref, atol=2e-4 * math.sqrt(K), rtol=1e-5)
+
+
+def gemm_ln(ring, mode, A, B, C, act=0, c1=None, c2=None, stats=None, eps=1e-12, bias=None, yr=None, st_in=None,
+            lg=None, lb=None):
+    M, K = A.shape
+    N = B.shape[0]
+    rc = _lib().fh_op_gemm_ln(ring, mode, ptr(A), ptr(B), ptr(c1), ptr(c2), ptr(stats), eps, ptr(bias), ptr(yr),
+                              ptr(st_in), ptr(lg), ptr(lb), ptr(C), M, N, K, act, None)
+    assert rc == 0
+    sync()
+    return C.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 384, 384), (1030, 1536, 384), (257, 384, 1536), (600, 1152, 384)])
+def test_gemm_ln_modes(M, N, K):
+    """The folded-LayerNorm GEMM forms: LN_IN (row statistics of A gathered
+    in the K loop, C = act(rstd·(A·Bᵀ − mean·c1) + c2)) and RES_LN (the
+    residual's LayerNorm rebuilt in the epilogue), on both kernels: the same
+    bits from each, within float tolerance of a float64 restatement."""
+    rng = np.random.default_rng(M + 3 * N + K)
+    y = (rng.standard_normal((M, K)) * 3 + 1.5).astype(np.float16)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    c1 = w.astype(np.float64).sum(1).astype(np.float32)
+    c2 = rng.standard_normal(N).astype(np.float32)
+    dy, dw = dev(y), dev(w)
+    wp = torch.empty_like(dw)
+    assert _lib().fh_op_ring_pack(ptr(dw), ptr(wp), N, K, None) == 0
+    y64 = y.astype(np.float64)
+    mean = y64.mean(1)
+    rstd = 1.0 / np.sqrt(y64.var(1) + 1e-5)
+    dot = y64 @ w.astype(np.float64).T
+    for act in (0, 1):
+        outs, stats = [], []
+        for ring, b in ((0, dw), (1, wp)):
+            C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            st = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+            outs.append(gemm_ln(ring, 1, dy, b, C, act, dev(c1), dev(c2), st, 1e-5))
+            stats.append(st.cpu().numpy())
+        assert np.array_equal(stats[0], stats[1]), ("stats", np.abs(stats[0] - stats[1]).max(0),
+                                                     int((stats[0] != stats[1]).any(1).sum()))
+        assert np.array_equal(outs[0], outs[1]), ("LN_IN", act, np.abs(outs[0].astype(np.float64) - outs[1]).max(),
+                                                  int((outs[0] != outs[1]).sum()))
+        np.testing.assert_allclose(stats[1][:, 0], mean, atol=1e-5, rtol=1e-5)
+        np.testing.assert_allclose(stats[1][:, 1], rstd, rtol=1e-4)
+        ref = rstd[:, None] * (dot - mean[:, None] * c1) + c2
+        if act:
+            ref = gelu64(ref)
+        np.testing.assert_allclose(outs[1].astype(np.float64), ref, atol=2e-3 * math.sqrt(K) / 4, rtol=2e-3)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    yr = (rng.standard_normal((M, N)) * 2 + 0.5).astype(np.float16)
+    yr64 = yr.astype(np.float64)
+    st_in = np.stack([yr64.mean(1), 1.0 / np.sqrt(yr64.var(1) + 1e-5)], 1).astype(np.float32)
+    lg = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    lb = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    da, dyr, dst, dlg, dlb, dbias = dev(a), dev(yr), dev(st_in), dev(lg), dev(lb), dev(bias)
+    outs = []
+    for ring, b in ((0, dw), (1, wp)):
+        C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        outs.append(gemm_ln(ring, 2, da, b, C, 0, bias=dbias, yr=dyr, st_in=dst, lg=dlg, lb=dlb))
+    assert np.array_equal(outs[0], outs[1]), ("RES_LN", np.abs(outs[0].astype(np.float64) - outs[1]).max())
+    st64 = st_in.astype(np.float64)
+    ref = a.astype(np.float64) @ w.astype(np.float64).T + bias + (yr64 - st64[:, :1]) * st64[:, 1:] * lg + lb
+    np.testing.assert_allclose(outs[1].astype(np.float64), ref, atol=2e-4 * math.sqrt(K) + 4e-3, rtol=1e-3)
+
+
+def test_gemm_ring_rejects_unfit_shapes():
+    d = dev(np.zeros((64, 64), np.float16))
+    c = torch.empty((64, 64), dtype=torch.float32, device="cuda")
+    from futon_amd import _lib as lib
+    # N % 128 != 0, K % 64 != 0, SwiGLU: not this kernel's shapes
+    assert _lib().fh_op_gemm_ring(ptr(d), ptr(d), None, None, 0, ptr(c), 64, 64, 64, 0, 1, None) == lib.FH_EINVAL
+    assert _lib().fh_op_gemm_ring(ptr(d), ptr(d), None, None, 0, ptr(c), 8, 128, 32, 0, 1, None) == lib.FH_EINVAL
+    assert _lib().fh_op_gemm_ring(ptr(d), ptr(d), None, None, 0, ptr(c), 8, 128, 64, 2, 1, None) == lib.FH_EINVAL
+
+
 @pytest.mark.parametrize("M,I,K", [(5, 32, 32), (70, 256, 64), (200, 1536, 384)])
 def test_gemm_swiglu_interleave(M, I, K):
     rng = np.random.default_rng(I + K)
