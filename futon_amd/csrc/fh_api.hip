@@ -107,8 +107,13 @@ struct DevMat {
     void *w = nullptr;       // f16 [n,k] or i8 [n,k]
     float *scale = nullptr;  // i8: [n]
     int n = 0, k = 0;
-    bool ring = false;       // rows stored in fh::ring_pack_row order, multiplied by fh::gemm_ring
+    void *wr = nullptr;      // f16 copy with rows in fh::ring_pack_row order for fh::gemm_ring, or null
 };
+
+// The persistent ring GEMM pays off once its 256×128 tiles cover about half
+// the CUs; fewer rows (small batches, the CLS-pooled last layer) run on the
+// tiled GEMM's smaller tiles with the natural-order copy.
+bool use_ring(const DevMat &w, int M) { return w.wr && (long)((M + 255) / 256) * (w.n / 128) >= 128; }
 
 struct DevLayer {
     DevMat qkv, out, ffn1, fc2;  // ffn1 = fc1, or fc1|gate interleaved in 16-row blocks (SwiGLU)
@@ -314,18 +319,18 @@ void fold_ln(std::vector<float> &w, int n, int k, const std::vector<float> &g, c
 }
 
 // Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales; with
-// ring, as f16 rows in fh::ring_pack_row order for fh::gemm_ring.
+// ring, also as f16 rows in fh::ring_pack_row order for fh::gemm_ring.
 int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8, bool ring = false) {
     d.n = n;
     d.k = k;
-    d.ring = ring && !q8;
-    if (d.ring) {
+    if (ring && !q8) {
         std::vector<uint16_t> h(w.size());
         for (int r = 0; r < n; r++) {
             const float *src = &w[(size_t)fh::ring_pack_row(r) * k];
             for (int j = 0; j < k; j++) h[(size_t)r * k + j] = f32_to_f16(src[j]);
         }
-        return upload(m, (uint16_t **)&d.w, h.data(), h.size() * 2);
+        const int rc = upload(m, (uint16_t **)&d.wr, h.data(), h.size() * 2);
+        if (rc) return rc;
     }
     if (q8) {
         std::vector<int8_t> codes((size_t)n * k);
@@ -497,7 +502,9 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
                          (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : resid_h ? (double)M * outn * 2 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(w.ring ? fh::gemm_ring(g, act, out_f32, s) : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
+    const bool ring = use_ring(w, M);
+    if (ring) g.B = w.wr;
+    LCHK(ring ? fh::gemm_ring(g, act, out_f32, s) : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
     return FH_OK;
 }
 
@@ -524,7 +531,9 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + (stats_out ? M * 8.0 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(w.ring ? fh::gemm_ring(g, act, false, s, fh::LN_IN) : fh::gemm_f16(g, act, false, s, fh::LN_IN));
+    const bool ring = use_ring(w, M);
+    if (ring) g.B = w.wr;
+    LCHK(ring ? fh::gemm_ring(g, act, false, s, fh::LN_IN) : fh::gemm_f16(g, act, false, s, fh::LN_IN));
     return FH_OK;
 }
 
@@ -551,7 +560,9 @@ int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, cons
     const double flops = 2.0 * M * (double)w.n * w.k;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * w.n * 4 + M * 8.0;
     Scope sc(m, cls, flops, bytes, s);
-    LCHK(w.ring ? fh::gemm_ring(g, fh::ACT_NONE, false, s, fh::RES_LN) : fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
+    const bool ring = use_ring(w, M);
+    if (ring) g.B = w.wr;
+    LCHK(ring ? fh::gemm_ring(g, fh::ACT_NONE, false, s, fh::RES_LN) : fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
     return FH_OK;
 }
 

@@ -41,6 +41,9 @@ struct Cfg {
     static constexpr int ACH = BM * CPR / NT;  // 16-byte A chunks per thread per slice
     static constexpr int BCH = BN * CPR / NT;
     static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/thread mismatch");
+    // The staged epilogue (32 rows per wave) and the LN row statistics fit in
+    // the operand LDS; small tiles store straight from registers.
+    static constexpr bool STAGE = (NT / 64) * 32 * (NTL * 16 * 4 + 16) + BM * 8 <= 2 * BM * ROW;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences
@@ -463,8 +466,6 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
 
     // Row statistics sit past the epilogue staging area of the A buffers.
     // Epilogue staging and row statistics reuse the A stages.
-    static_assert((C::NT / 64) * 32 * (C::NTL * 16 * 4 + 16) + C::BM * 8 <= 2 * C::BM * C::ROW,
-                  "epilogue staging exceeds LDS");
     f32x2 *rowstat = (f32x2 *)(&As[0][0] + 2 * C::BM * C::ROW - C::BM * 8);
     if (LNM == fh::LN_IN) {
         const float invk = 1.0f / (float)g.K;
@@ -480,10 +481,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
         }
         lds_barrier();
     }
-    if (KFULL && g.epi_lds)
-        store_tiles_lds<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0], rowstat);
-    else
-        store_tiles<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, acc, iacc, rowstat);
+    if constexpr (C::STAGE) {
+        if (KFULL && g.epi_lds) {
+            store_tiles_lds<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0], rowstat);
+            return;
+        }
+    }
+    store_tiles<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, acc, iacc, rowstat);
 }
 
 // Tile configurations (block tile, wave grid, row pad, prefetch depth).
@@ -492,6 +496,7 @@ using C1 = Cfg<128, 128, 2, 2, 32, 1>;
 using C2 = Cfg<256, 128, 4, 2, 32, 1>;
 using C3 = Cfg<256, 128, 4, 2, 32, 2>;
 using C5 = Cfg<256, 256, 2, 4, 32, 1>;
+using C6 = Cfg<64, 64, 2, 2, 16, 2>;
 
 template <class C, bool I8, bool KFULL, int ACT, bool OUT_F32, int LNM>
 void launch_one(const GemmArgs &g, hipStream_t s) {
@@ -533,7 +538,7 @@ hipError_t launch_cfg(const GemmArgs &ga, int act, bool out_f32, int ln, hipStre
     return hipGetLastError();
 }
 
-// FUTON_GEMM_TILE=0,1,2,3,5 pins a configuration (tuning knob); otherwise
+// FUTON_GEMM_TILE=0,1,2,3,5,6 pins a configuration (tuning knob); otherwise
 // the choice depends only on the problem shape.
 int forced_cfg() {
     static const int v = [] {
@@ -556,19 +561,23 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // statistics need whole 128-byte slices
     if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, ln, s);
     int cfg = forced_cfg();
-    if (cfg < 0 || cfg > 5 || cfg == 4) {
+    if (cfg < 0 || cfg > 6 || cfg == 4) {
         // 256×256 when it still gives every CU a block; 256×128 down to half
         // the CUs (it beats 128×128 on the N = H projections even there).
-        const long m256 = (g.M + 255) / 256;
+        // 64×64 when even 128×128 leaves most CUs idle (the few-row GEMMs of
+        // the CLS-pooled last layer).
+        const long m256 = (g.M + 255) / 256, m128 = (g.M + 127) / 128;
         if (g.N % 256 == 0 && m256 * (g.N / 256) >= 256) cfg = 5;
         else if (m256 * ((g.N + 127) / 128) >= 128) cfg = 3;
-        else cfg = 0;
+        else if (m128 * ((g.N + 127) / 128) >= 64) cfg = 0;
+        else cfg = 6;
     }
     switch (cfg) {
     case 1: return launch_cfg<C1, I8, true>(g, act, out_f32, ln, s);
     case 2: return launch_cfg<C2, I8, true>(g, act, out_f32, ln, s);
     case 3: return launch_cfg<C3, I8, true>(g, act, out_f32, ln, s);
     case 5: return launch_cfg<C5, I8, true>(g, act, out_f32, ln, s);
+    case 6: return launch_cfg<C6, I8, true>(g, act, out_f32, ln, s);
     default: return launch_cfg<C0, I8, true>(g, act, out_f32, ln, s);
     }
 }
