@@ -110,10 +110,10 @@ struct DevMat {
     void *wr = nullptr;      // f16 copy with rows in fh::ring_pack_row order for fh::gemm_ring, or null
 };
 
-// The persistent ring GEMM pays off once its 256×128 tiles cover about half
-// the CUs; fewer rows (small batches, the CLS-pooled last layer) run on the
+// The persistent ring GEMM pays off once its tiles cover about half the
+// CUs; fewer rows (small batches, the CLS-pooled last layer) run on the
 // tiled GEMM's smaller tiles with the natural-order copy.
-bool use_ring(const DevMat &w, int M) { return w.wr && (long)((M + 255) / 256) * (w.n / 128) >= 128; }
+bool use_ring(const DevMat &w, int M) { return w.wr && fh::gemm_ring_worth(M, w.n); }
 
 struct DevLayer {
     DevMat qkv, out, ffn1, fc2;  // ffn1 = fc1, or fc1|gate interleaved in 16-row blocks (SwiGLU)
@@ -128,11 +128,12 @@ struct DevLayer {
 enum KClass {
     K_EMBED, K_GEMM_QKV, K_ATTN, K_GEMM_OUT, K_LN, K_GEMM_FFN1, K_GEMM_FC2, K_QUANT, K_GATHER, K_POOL,
     K_CLS_TAIL,  // last CLS layer after its QKV GEMM: attention for row 0 and every M = nseq launch
+    K_STATS,     // row statistics for the folded LayerNorms
     K_NCLASS
 };
 const char *kClassNames[K_NCLASS] = {"embed_ln",  "gemm_qkv", "attention", "gemm_out",
                                      "layer_norm", "gemm_ffn1", "gemm_fc2", "quantize_rows",
-                                     "gather_cls", "pool_l2",    "cls_last_layer"};
+                                     "gather_cls", "pool_l2",    "cls_last_layer", "row_stats"};
 
 struct ProfPending {
     int cls;
@@ -508,11 +509,19 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     return FH_OK;
 }
 
+// (mean, rstd) of y's rows for the GEMMs that fold LN(y).
+int row_stats(fh_model *m, int cls, const f16 *y, int M, f32x2 *st, hipStream_t s) {
+    const int H = m->cfg.hidden_size;
+    Scope sc(m, cls, 0.0, (double)M * H * 2 + M * 8.0, s);
+    LCHK(fh::row_stats(y, M, H, (float)m->cfg.layer_norm_eps, st, s));
+    return FH_OK;
+}
+
 // Binary16 GEMM whose A operand is the un-normalized input y of a folded
-// LayerNorm (LN_IN): C = act(rstd·(y·W'ᵀ − mean·c1) + c2); the row statistics
-// of y go to stats_out.
+// LayerNorm (LN_IN): C = act(rstd·(y·W'ᵀ − mean·c1) + c2), with y's row
+// statistics from row_stats.
 int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const float *c1, const float *c2,
-              f32x2 *stats_out, void *C, int ldc, int act, hipStream_t s) {
+              const f32x2 *stats, void *C, int ldc, int act, hipStream_t s) {
     GemmArgs g{};
     g.A = y;
     g.B = w.w;
@@ -525,11 +534,10 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     g.ldc = ldc;
     g.c1 = c1;
     g.c2 = c2;
-    g.stats_out = stats_out;
-    g.ln_eps = (float)m->cfg.layer_norm_eps;
+    g.stats_in = stats;
     const double flops = 2.0 * M * (double)w.n * w.k;
     const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
-    const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + (stats_out ? M * 8.0 : 0.0);
+    const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + M * 8.0;
     Scope sc(m, cls, flops, bytes, s);
     const bool ring = use_ring(w, M);
     if (ring) g.B = w.wr;
@@ -538,7 +546,8 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
 }
 
 // Binary16 GEMM with the residual LN(yr) rebuilt in the epilogue (RES_LN):
-// C = f16(A·Wᵀ + bias + (yr − mean)·rstd·γ + β).
+// C = f16(A·Wᵀ + bias + (yr − mean)·rstd·γ + β), yr's statistics from
+// row_stats.
 int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, const float *bias, const f16 *yr,
                const f32x2 *stats, const float *gamma, const float *beta, f16 *C, hipStream_t s) {
     GemmArgs g{};
@@ -583,11 +592,12 @@ int layer_norm(fh_model *m, int cls, const float *y32, const f16 *y16, int M, co
 // Forward with every LayerNorm but the last folded into the GEMMs (binary16
 // path).  The residual stream is carried un-normalized: yA (x16) is the input
 // of the LayerNorm that feeds the attention block (the embedding sum, then
-// each layer's y2), yB (y32's storage) the input of norm1.  The QKV and FFN1
-// GEMMs normalize on the fly (LN_IN) and record (mean, rstd) per row; the
-// output projection and FC2 rebuild their residual LN(y) from those (RES_LN)
-// and write the next un-normalized y.  Only the last layer's norm2 runs as a
-// kernel, producing the f32 rows pooling reads.
+// each layer's y2), yB (y32's storage) the input of norm1.  A small kernel
+// records (mean, rstd) per row of y; the QKV and FFN1 GEMMs normalize on the
+// fly with them (LN_IN), and the output projection and FC2 rebuild their
+// residual LN(y) from the same statistics (RES_LN) and write the next
+// un-normalized y.  Only the last layer's norm2 runs as a kernel, producing
+// the f32 rows pooling reads.
 int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
     const fh_config &c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, T = b.T, S = b.nseq;
@@ -607,7 +617,8 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const float *bA = li ? m->layers[(size_t)li - 1].n2b : m->emb_b;
 
         // qkv = LN(yA)·Wqkvᵀ + b  (model.go:555)
-        if ((rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
+        if ((rc = row_stats(m, K_STATS, m->x16, T, m->sA, s)) ||
+            (rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
                             s)))
             return rc;
 
@@ -647,7 +658,8 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // h = act(LN1(yB)·W1ᵀ + b1); yA = h·W2ᵀ + b2 + LN1(yB)  (model.go:607-633)
-        if ((rc = gemm_lnin(m, kFfn1, L.ffn1, yBo, M, L.ffn1_c1, L.ffn1_c2, sB, m->hbuf, I,
+        if ((rc = row_stats(m, last_cls ? K_CLS_TAIL : K_STATS, yBo, M, sB, s)) ||
+            (rc = gemm_lnin(m, kFfn1, L.ffn1, yBo, M, L.ffn1_c1, L.ffn1_c2, sB, m->hbuf, I,
                             swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU, s)))
             return rc;
         if ((rc = gemm_resln(m, kFc2, L.fc2, m->hbuf, M, L.fc2_b, yBo, sB, L.n1w, L.n1b, yA, s))) return rc;
@@ -935,9 +947,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                     (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
                     return bail(rc);
             }
-            // FFN1 stays on the tiled GEMM: its 256×256 tiles amortize the
-            // GELU epilogue better than the ring's 256×128 ones.
-            if ((rc = upload_mat(m, L.ffn1, w, I, H, q8))) return bail(rc);
+            if ((rc = upload_mat(m, L.ffn1, w, I, H, q8, ring_fits(I, H)))) return bail(rc);
             if ((rc = ld.vec_f32(nm("mlp.fc1.bias"), I, &L.ffn1_b, true))) return bail(rc);
         }
         if ((rc = ld.mat_host(nm("mlp.fc2.weight"), H, I, w)) ||

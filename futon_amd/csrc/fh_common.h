@@ -42,9 +42,7 @@ struct GemmArgs {
     // un-normalized LN input y; x = (y − mean)·rstd·γ + β is never stored):
     const float *c1;     // LN_IN: [N] Σ_k B[n,k] (B = W·diag(γ), as stored)
     const float *c2;     // LN_IN: [N] Σ_k W[n,k]·β[k] + bias[n]
-    f32x2 *stats_out;    // LN_IN: [M] (mean, rstd) of A's rows, or null
-    float ln_eps;        // LN_IN
-    const f32x2 *stats_in;      // RES_LN: [M] (mean, rstd) of resid_h's rows
+    const f32x2 *stats_in;      // [M] (mean, rstd) of A's rows (LN_IN) or of resid_h's rows (RES_LN)
     const float *ln_g, *ln_b;   // RES_LN: γ, β of resid_h's LayerNorm
 };
 
@@ -67,7 +65,7 @@ namespace fh {
 enum Act { ACT_NONE = 0, ACT_GELU = 1, ACT_SWIGLU = 2, ACT_RES16 = 3 };
 // LayerNorm folding of a binary16 GEMM: LN_IN — A is the LN input y, B the
 // weights scaled by γ, and the epilogue forms rstd·(acc − mean·c1) + c2 with
-// row statistics gathered while A streams through; RES_LN — the residual is
+// y's row statistics from stats_in (row_stats); RES_LN — the residual is
 // LN(resid_h) rebuilt from stats_in, γ, β (binary16 output with ACT_NONE).
 enum LnMode { LN_NONE = 0, LN_IN = 1, RES_LN = 2 };
 hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);
@@ -76,6 +74,8 @@ hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 // ring_pack_row (rows permuted inside each 64-row block); gemm_ring_ok says
 // whether a problem fits it (binary16, N % 128 == 0, K % 64 == 0, no SwiGLU).
 bool gemm_ring_ok(const GemmArgs &a, int act, bool out_f32, int ln);
+// Whether an M×N problem has enough rows for the ring to beat the tiled GEMM.
+bool gemm_ring_worth(int M, int N);
 hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);
 // out = B with rows in ring_pack_row order (N % 64 == 0, K % 8 == 0).
 hipError_t ring_pack(const f16 *B, f16 *out, int N, int K, hipStream_t s);
@@ -93,6 +93,10 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
 // y32 or y16 (exactly one non-null) holds proj + bias + residual.
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
                       float eps, float *x32, f16 *x16, hipStream_t s);
+// (mean, rstd) of each binary16 row of y [M, H] (H in {256, 384, 512, 768,
+// 1024}): float64 Σy and Σy², rounded to float32 like layerNormRows' float64
+// statistics.
+hipError_t row_stats(const f16 *y, int M, int H, float eps, f32x2 *st, hipStream_t s);
 // Sequence i's first row (and its (mean, rstd) when st is non-null) → row i.
 hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const int32_t *offsets, int nseq, int H,
                        float *xc32, f16 *xc16, f32x2 *stc, hipStream_t s);

@@ -67,10 +67,10 @@ extern "C" int fh_op_gemm_ring(const void *A, const void *B_packed, const float 
 }
 
 extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const void *B, const float *c1,
-                             const float *c2, void *stats_out, float eps, const float *bias, const void *resid_h,
-                             const void *stats_in, const float *ln_g, const float *ln_b, void *C, int32_t M,
-                             int32_t N, int32_t K, int32_t act, void *stream) {
-    if (!A || !B || !C || M < 0 || N <= 0 || K <= 0 || K % 64 || N % 4) return FH_EINVAL;
+                             const float *c2, const float *bias, const void *resid_h, const void *stats,
+                             const float *ln_g, const float *ln_b, void *C, int32_t M, int32_t N, int32_t K,
+                             int32_t act, void *stream) {
+    if (!A || !B || !C || !stats || M < 0 || N <= 0 || K <= 0 || K % 64 || N % 4) return FH_EINVAL;
     GemmArgs g{};
     g.A = A;
     g.B = B;
@@ -82,19 +82,17 @@ extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const
     g.ldb = K;
     g.ldc = N;
     g.ldr = N;
+    g.stats_in = (const f32x2 *)stats;
     int a;
     if (ln_mode == fh::LN_IN) {
         if (!c1 || !c2 || (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU)) return FH_EINVAL;
         g.c1 = c1;
         g.c2 = c2;
-        g.stats_out = (f32x2 *)stats_out;
-        g.ln_eps = eps;
         a = act;
     } else if (ln_mode == fh::RES_LN) {
-        if (!resid_h || !stats_in || !ln_g || !ln_b || act != FH_OP_ACT_NONE) return FH_EINVAL;
+        if (!resid_h || !ln_g || !ln_b || act != FH_OP_ACT_NONE) return FH_EINVAL;
         g.bias = bias;
         g.resid_h = (const f16 *)resid_h;
-        g.stats_in = (const f32x2 *)stats_in;
         g.ln_g = ln_g;
         g.ln_b = ln_b;
         a = fh::ACT_RES16;
@@ -108,6 +106,11 @@ extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const
         return code_of(fh::gemm_ring(g, a, false, s, ln_mode));
     }
     return code_of(fh::gemm_f16(g, ln_mode == fh::RES_LN ? (int)fh::ACT_NONE : a, false, s, ln_mode));
+}
+
+extern "C" int fh_op_row_stats(const void *y, int32_t M, int32_t H, float eps, void *stats, void *stream) {
+    if (!y || !stats || M < 0 || (H != 256 && H != 384 && H != 512 && H != 768 && H != 1024)) return FH_EINVAL;
+    return code_of(fh::row_stats((const f16 *)y, M, H, eps, (f32x2 *)stats, (hipStream_t)stream));
 }
 
 extern "C" int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream) {

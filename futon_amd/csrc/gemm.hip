@@ -41,9 +41,9 @@ struct Cfg {
     static constexpr int ACH = BM * CPR / NT;  // 16-byte A chunks per thread per slice
     static constexpr int BCH = BN * CPR / NT;
     static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "tile/thread mismatch");
-    // The staged epilogue (32 rows per wave) and the LN row statistics fit in
-    // the operand LDS; small tiles store straight from registers.
-    static constexpr bool STAGE = (NT / 64) * 32 * (NTL * 16 * 4 + 16) + BM * 8 <= 2 * BM * ROW;
+    // The staged epilogue (32 rows per wave) fits in the operand LDS; small
+    // tiles store straight from registers.
+    static constexpr bool STAGE = (NT / 64) * 32 * (NTL * 16 * 4 + 16) <= 2 * BM * ROW;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences
@@ -67,6 +67,7 @@ __device__ __forceinline__ void tile_coords(int &mt, int &nt) {
     nt = logical - mt * gx;
 }
 
+// rs: (mean, rstd) of A's row (LN_IN) or of the residual's row (RES_LN).
 template <int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int col, f32x4 v,
                                                f32x4 gate, f32x2 rs) {
@@ -101,7 +102,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
         v += *(const f32x4 *)(g.resid + (size_t)row * g.ldr + col);
     } else if (g.resid_h) {
         const f16x4 r = *(const f16x4 *)(g.resid_h + (size_t)row * g.ldr + col);
-        if (LNM == fh::RES_LN) v += ln_resid(g, row, col, r);
+        if (LNM == fh::RES_LN) v += ln_resid(g, rs, col, r);
         else v += (f32x4){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
     }
     if (OUT_F32) {
@@ -116,14 +117,13 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
 // row = tile_m + lane%16, col = tile_n + (lane/16)·4.
 template <class C, bool I8, int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
-                                            const f32x4 (&acc)[C::NTL][C::MT], const i32x4 (&iacc)[C::NTL][C::MT],
-                                            const f32x2 *rowstat) {
+                                            const f32x4 (&acc)[C::NTL][C::MT], const i32x4 (&iacc)[C::NTL][C::MT]) {
 #pragma unroll
     for (int tm = 0; tm < C::MT; ++tm) {
         const int rl = (wm * C::MT + tm) * 16 + (lane & 15);
         const int row = m0 + rl;
         if (row >= g.M) continue;
-        const f32x2 rs = LNM == fh::LN_IN ? rowstat[rl] : (f32x2){0.f, 0.f};
+        const f32x2 rs = LNM != fh::LN_NONE ? g.stats_in[row] : (f32x2){0.f, 0.f};
         float sa = 0.f;
         if (I8) sa = g.a_scale[row];
 #pragma unroll
@@ -161,8 +161,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, i
 template <class C, bool I8, int ACT, bool OUT_F32, int LNM>
 __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n0, int wm, int wn, int lane,
                                                 int wave, const f32x4 (&acc)[C::NTL][C::MT],
-                                                const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds,
-                                                const f32x2 *rowstat) {
+                                                const i32x4 (&iacc)[C::NTL][C::MT], uint8_t *lds) {
     static_assert(C::MT % 2 == 0 && C::NTL % 2 == 0, "staged epilogue works on 32-row, 32-column multiples");
     constexpr int WTN = C::NTL * 16;                           // wave tile width
     constexpr int OC = ACT == fh::ACT_SWIGLU ? WTN / 2 : WTN;  // output columns per wave
@@ -179,7 +178,7 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
             const int tm = 2 * p + h;
             const int rl = (wm * C::MT + tm) * 16 + (lane & 15);
             const int row = m0 + rl;
-            const f32x2 rs = LNM == fh::LN_IN ? rowstat[rl] : (f32x2){0.f, 0.f};
+            const f32x2 rs = LNM == fh::LN_IN ? g.stats_in[min(row, g.M - 1)] : (f32x2){0.f, 0.f};
             float sa = 0.f;
             if (I8) sa = g.a_scale[min(row, g.M - 1)];
 #pragma unroll
@@ -246,8 +245,9 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                     const f16x8 rr = *(const f16x8 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
                     const f16x4 ra = {rr[0], rr[1], rr[2], rr[3]}, rb = {rr[4], rr[5], rr[6], rr[7]};
                     if (LNM == fh::RES_LN) {
-                        r0 = ln_resid(g, grow, gcol, ra);
-                        r1 = ln_resid(g, grow, gcol + 4, rb);
+                        const f32x2 st = g.stats_in[grow];
+                        r0 = ln_resid(g, st, gcol, ra);
+                        r1 = ln_resid(g, st, gcol + 4, rb);
                     } else {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
@@ -288,14 +288,6 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
             *(i32x4 *)((uint8_t *)g.C + ((size_t)grow * g.ldc + gcol) * ESZ) = d;
         }
     }
-}
-
-// DPP sum over each aligned group of 8 lanes (xor 1, xor 2, half-row mirror).
-__device__ __forceinline__ float sum8_lanes(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    return v;
 }
 
 // amdgpu_waves_per_eu(1): one block of 2–8 waves fills a CU's LDS anyway, so
@@ -356,29 +348,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
             }
         }
     };
-    // LN_IN: Σy and Σy² of this thread's 8-element pieces of its A rows, over
-    // the slices it stores (each stored exactly once); f16 products are exact.
-    float ssum[C::ACH], ssq[C::ACH];
-#pragma unroll
-    for (int i = 0; i < C::ACH; ++i) ssum[i] = ssq[i] = 0.f;
-    auto sstore = [&](int st, int buf, bool fresh) {
+    auto sstore = [&](int st, int buf) {
 #pragma unroll
         for (int i = 0; i < C::ACH; ++i) {
             const int c = tid + i * C::NT;
             *(i32x4 *)&As[buf][(c / C::CPR) * C::ROW + (c % C::CPR) * 16] = ra[st][i];
-        }
-        if (LNM == fh::LN_IN && fresh) {
-            const f16x2 one = {(f16)1.0f, (f16)1.0f};
-#pragma unroll
-            for (int i = 0; i < C::ACH; ++i) {
-                const f16x8 h = __builtin_bit_cast(f16x8, ra[st][i]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f16x2 pr = {h[2 * j], h[2 * j + 1]};
-                    ssum[i] = __builtin_amdgcn_fdot2(pr, one, ssum[i], false);
-                    ssq[i] = __builtin_amdgcn_fdot2(pr, pr, ssq[i], false);
-                }
-            }
         }
 #pragma unroll
         for (int i = 0; i < C::BCH; ++i) {
@@ -431,14 +405,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
     if (C::PF == 1) {
         // One register stage: slice kt+1 is fetched while slice kt is multiplied.
         gload(0, 0);
-        sstore(0, 0, true);
+        sstore(0, 0);
         lds_barrier();
         for (int kt = 0; kt < nk; ++kt) {
             gload(0, min((kt + 1) * KB, last));
             __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
             compute(kt & 1);
             __builtin_amdgcn_sched_barrier(0);
-            sstore(0, (kt + 1) & 1, kt + 1 < nk);
+            sstore(0, (kt + 1) & 1);
             lds_barrier();
         }
     } else {
@@ -449,12 +423,12 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
             __builtin_amdgcn_sched_barrier(0);     // keep the prefetch ahead of the MFMAs
             compute(par);
             __builtin_amdgcn_sched_barrier(0);
-            sstore(par ^ 1, par ^ 1, kt + 1 < nk);
+            sstore(par ^ 1, par ^ 1);
             lds_barrier();
         };
         gload(0, 0);
         gload(1, min(KB, last));
-        sstore(0, 0, true);
+        sstore(0, 0);
         lds_barrier();
         int kt = 0;
         for (; kt + 1 < nk; kt += 2) {
@@ -464,30 +438,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1))) void
         if (kt < nk) step(kt, 0);
     }
 
-    // Row statistics sit past the epilogue staging area of the A buffers.
-    // Epilogue staging and row statistics reuse the A stages.
-    f32x2 *rowstat = (f32x2 *)(&As[0][0] + 2 * C::BM * C::ROW - C::BM * 8);
-    if (LNM == fh::LN_IN) {
-        const float invk = 1.0f / (float)g.K;
-#pragma unroll
-        for (int i = 0; i < C::ACH; ++i) {
-            const float s = sum8_lanes(ssum[i]), q = sum8_lanes(ssq[i]);
-            const int rl = (tid + i * C::NT) / C::CPR;
-            if ((tid % C::CPR) == 0) {
-                const f32x2 st = ln_stats(s, q, invk, g.ln_eps);
-                rowstat[rl] = st;
-                if (g.stats_out && nt == 0 && m0 + rl < g.M) g.stats_out[m0 + rl] = st;
-            }
-        }
-        lds_barrier();
-    }
+    // The staged epilogue reuses the A stages.
     if constexpr (C::STAGE) {
         if (KFULL && g.epi_lds) {
-            store_tiles_lds<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0], rowstat);
+            store_tiles_lds<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, wave, acc, iacc, &As[0][0]);
             return;
         }
     }
-    store_tiles<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, acc, iacc, rowstat);
+    store_tiles<C, I8, ACT, OUT_F32, LNM>(g, m0, n0, wm, wn, lane, acc, iacc);
 }
 
 // Tile configurations (block tile, wave grid, row pad, prefetch depth).
@@ -558,7 +516,7 @@ hipError_t launch(const GemmArgs &ga, int act, bool out_f32, int ln, hipStream_t
     g.epi_lds = (nout % (act == fh::ACT_SWIGLU ? 32 : 64) == 0) && (g.N % 64 == 0) &&
                 (out_f32 || act == fh::ACT_RES16 || !has_res) && (g.ldc % 8 == 0) && (!has_res || g.ldr % 8 == 0);
     const bool kfull = (g.K * (I8 ? 1 : 2)) % KFULL_BYTES == 0;
-    if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // statistics need whole 128-byte slices
+    if (ln == fh::LN_IN && !kfull) return hipErrorInvalidValue;  // the LN_IN kernels are built for whole slices
     if (!kfull) return launch_cfg<C0, I8, false>(g, act, out_f32, ln, s);
     int cfg = forced_cfg();
     if (cfg < 0 || cfg > 6 || cfg == 4) {

@@ -37,12 +37,6 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // uncontracted products), so that each GEMM kernel computes them bit for bit
 // alike whatever the compiler's contraction choices in its context.
 
-// (mean, rstd) of a row from Σy and Σy² over k = 1/invk elements.
-__device__ __forceinline__ f32x2 ln_stats(float s, float q, float invk, float eps) {
-    const float mean = s * invk;
-    const float var = fmaxf(fmaf(q, invk, -__fmul_rn(mean, mean)), 0.f);
-    return (f32x2){mean, 1.0f / sqrtf(var + eps)};
-}
 // LN_IN fold of one 4-column group: rstd·(acc − mean·c1) + c2.
 __device__ __forceinline__ f32x4 ln_fold_v(f32x4 v, f32x2 rs, f32x4 c1, f32x4 c2) {
 #pragma unroll
@@ -59,8 +53,8 @@ __device__ __forceinline__ f32x4 ln_resid_v(f16x4 y, f32x2 st, f32x4 gm, f32x4 b
     for (int i = 0; i < 4; ++i) r[i] = fmaf(__fmul_rn((float)y[i] - st[0], st[1]), gm[i], bt[i]);
     return r;
 }
-__device__ __forceinline__ f32x4 ln_resid(const GemmArgs &g, int row, int col, f16x4 y) {
-    return ln_resid_v(y, g.stats_in[row], *(const f32x4 *)(g.ln_g + col), *(const f32x4 *)(g.ln_b + col));
+__device__ __forceinline__ f32x4 ln_resid(const GemmArgs &g, f32x2 st, int col, f16x4 y) {
+    return ln_resid_v(y, st, *(const f32x4 *)(g.ln_g + col), *(const f32x4 *)(g.ln_b + col));
 }
 
 }  // namespace fh_epi

@@ -22,8 +22,8 @@
 //   two whole 16-byte runs of 8 features: coalesced stores straight from
 //   registers, no LDS staging.
 // The accumulation order over K is the one gemm.hip uses (same slices, same
-// MFMA shape, same LN statistics reduction), so both kernels give the same
-// bits for the same operands.
+// MFMA shape) and the epilogue arithmetic is shared, so both kernels give the
+// same bits for the same operands.
 #include <cstdlib>
 
 #include "fh_common.h"
@@ -32,38 +32,50 @@
 namespace {
 using namespace fh_epi;
 
-constexpr int BM = 256, BN = 128, WM = 4, WN = 2, SLOTS = 3;
-constexpr int NT = 64 * WM * WN;                  // 512 threads
-constexpr int MT = BM / WM / 16;                  // token tiles per wave (4)
-constexpr int NTL = BN / WN / 16;                 // feature tiles per wave (4: the 64-row packing block)
-constexpr int ROWB = 128;                         // bytes of K per slice row (64 f16)
-constexpr int STAGE = (BM + BN) * ROWB;           // bytes per ring slot
-constexpr int DPW = (BM + BN) / 8 / (WM * WN);    // 1-KB DMA blocks per wave per slice
-static_assert(NTL == 4 && DPW * 8 * WM * WN == BM + BN && BM % 8 == 0, "tile shape");
+constexpr int ROWB = 128;  // bytes of K per slice row (64 f16)
 
-// Buffer resource for raw 16-byte loads of `bytes` bytes at p: offsets at or
-// beyond `bytes` read as zero.
-__device__ __forceinline__ i32x4 buf_rsrc(const void *p, uint32_t bytes) {
-    const uint64_t a = (uint64_t)p;
-    return (i32x4){(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+// Ring configuration: BM×BN output tile, WM×WN waves, SLOTS ring slots;
+// PERSIST: one block per CU looping over tiles (else one block per tile,
+// the hardware scheduling them as CUs free up).
+template <int BM_, int BN_, int WM_, int WN_, int SLOTS_, bool PERSIST_>
+struct RCfg {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SLOTS = SLOTS_;
+    static constexpr bool PERSIST = PERSIST_;
+    static constexpr int NT = 64 * WM * WN;                // threads
+    static constexpr int MT = BM / WM / 16;                // token tiles per wave
+    static constexpr int NTL = BN / WN / 16;               // feature tiles per wave (the 64-row packing block)
+    static constexpr int STAGE = (BM + BN) * ROWB;         // bytes per ring slot
+    static constexpr int DPW = (BM + BN) / 8 / (WM * WN);  // 1-KB DMA blocks per wave per slice
+    static constexpr int BPC = 163840 / (SLOTS * STAGE);   // blocks per CU the LDS allows
+    static_assert(NTL == 4 && DPW * 8 * WM * WN == BM + BN && BM % 8 == 0 && SLOTS >= 2 && BPC >= 1,
+                  "ring tile shape");
+};
+constexpr int BN = 128;     // every configuration's column tile (the packing unit × 2)
+constexpr int BM_MAX = 256;
+
+// Buffer resource for raw loads and stores of `bytes` bytes at p: offsets
+// at or beyond `bytes` read as zero and are not written.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// 16 bytes per lane from rs + voff + soff into LDS at lds_addr + lane·16.
-// Issued as inline assembly: the compiler does not track LDS written by the
-// DMA path, so the ring's waits are explicit (s_waitcnt vmcnt + barrier).
-__device__ __forceinline__ void dma16(i32x4 rs, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds_addr), "v"(voff), "s"(rs), "s"(soff)
-                 : "memory", "m0");
+// 16 bytes per lane from rs + voff + soff into LDS at lds_addr + lane·16
+// (buffer_load_dwordx4 … lds).  The ring orders these against its LDS reads
+// itself (s_waitcnt vmcnt + barrier); the compiler counts them in vmcnt.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(uintptr_t)lds_addr, 16,
+                                             voff, soff, 0, 0);
 }
 
 // RES: no residual (0), f32 (1) or binary16 (2); BIAS: g.bias is set.  The
 // epilogue is straight-line code for each combination, so the number of
 // vector memory instructions it issues is a constant the ring's waits use.
-template <int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ring_kernel(GemmArgs g, int ntn,
-                                                                                           int per_xcd) {
+template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+__global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void ring_kernel(GemmArgs g, int ntn,
+                                                                                              int per_xcd) {
+    constexpr int BM = R::BM, WN = R::WN, SLOTS = R::SLOTS;
+    constexpr int MT = R::MT, NTL = R::NTL, STAGE = R::STAGE, DPW = R::DPW;
+    static_assert(R::BN == BN, "column tile");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[SLOTS * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -81,8 +93,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
     if (nsl == 0) return;
 
     const uint32_t lda_b = (uint32_t)g.lda * 2, ldb_b = (uint32_t)g.ldb * 2;
-    const i32x4 rA = buf_rsrc(g.A, (uint32_t)g.M * lda_b);
-    const i32x4 rB = buf_rsrc(g.B, (uint32_t)g.N * ldb_b);
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(g.A, (uint32_t)g.M * lda_b);
+    const __amdgpu_buffer_rsrc_t rB = buf_rsrc(g.B, (uint32_t)g.N * ldb_b);
     const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
 
     // DMA block b of a slot holds slot rows 8b..8b+7 (rows < BM: A, else B);
@@ -110,7 +122,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
             const uint32_t b = (uint32_t)(wave * DPW + i);
             const uint32_t dst = slot + b * 1024;
             const uint32_t voff = isA[i] ? offA + b * 8 * lda_b : offB + b * 8 * ldb_b;
-            dma16(isA[i] ? rA : rB, dst, voff, soff);
+            if (isA[i]) dma16(rA, dst, voff, soff);
+            else dma16(rB, dst, voff, soff);
         }
     };
 
@@ -122,16 +135,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
     const int abase = wm * MT * 16 * ROWB, bbase = BM * ROWB + wn * NTL * 16 * ROWB;
 
     f32x4 acc[NTL][MT];
-    float ssum[2][MT], ssq[2][MT];  // LN_IN: per chunk-of-8 partial sums of this lane's rows
     auto clear = [&] {
 #pragma unroll
         for (int a = 0; a < NTL; ++a)
 #pragma unroll
             for (int b = 0; b < MT; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int b = 0; b < MT; ++b) ssum[ks][b] = ssq[ks][b] = 0.f;
     };
     clear();
 
@@ -144,19 +152,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
             for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(base + abase + t * 16 * ROWB + fo[ks]);
 #pragma unroll
             for (int t = 0; t < NTL; ++t) bf[t] = *(const i32x4 *)(base + bbase + t * 16 * ROWB + fo[ks]);
-            if (LNM == fh::LN_IN) {
-                const f16x2 one = {(f16)1.0f, (f16)1.0f};
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const f16x8 h = __builtin_bit_cast(f16x8, af[t]);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const f16x2 pr = {h[2 * q], h[2 * q + 1]};
-                        ssum[ks][t] = __builtin_amdgcn_fdot2(pr, one, ssum[ks][t], false);
-                        ssq[ks][t] = __builtin_amdgcn_fdot2(pr, pr, ssq[ks][t], false);
-                    }
-                }
-            }
 #pragma unroll
             for (int tn = 0; tn < NTL; ++tn)
 #pragma unroll
@@ -167,7 +162,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
     };
 
     // Epilogue of tile ti, in two parts.  epi_load issues the loads the
-    // epilogue needs (column constants, binary16 residual rows, statistics)
+    // epilogue needs (column constants, binary16 residual rows, row statistics)
     // before the ring's DMA of the tile's last slice: a wait for a load queued
     // behind those DMAs would also wait for them.  epi_store does the
     // arithmetic, gemm.hip's epilogue_store term for term, and the stores:
@@ -175,13 +170,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
     // every wave issues exactly NSTORE of them.
     // This lane's 16 features: cb + 32·h + 4·half + {0..3}, q = 2·h + half.
     constexpr int ESZ = OUT_F32 ? 4 : 2;
-    const __amdgpu_buffer_rsrc_t rC =
-        __builtin_amdgcn_make_buffer_rsrc(g.C, (short)0, (int)((uint32_t)g.M * (uint32_t)g.ldc * ESZ), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
-        g.stats_out ? (void *)g.stats_out : g.C, (short)0, g.stats_out ? g.M * 8 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rC = buf_rsrc(g.C, (uint32_t)g.M * (uint32_t)g.ldc * ESZ);
     f32x4 k1[4], k2[4], kb[4], kg[4], kt[4];
     f16x8 rh[MT][2];
-    f32x2 sti[MT];
+    f32x2 sti[MT];  // (mean, rstd) of the row: A's (LN_IN) or the residual's (RES_LN)
     auto tile_of = [&](int ti, int &m0, int &nt) {
         const int t = t0 + ti * nbx;
         const int mt = t / ntn;
@@ -213,7 +205,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
 #pragma unroll
                 for (int h = 0; h < 2; ++h) rh[tm][h] = *(const f16x8 *)(g.resid_h + (size_t)rr * g.ldr + cb + h * 32);
             }
-            if (LNM == fh::RES_LN) sti[tm] = g.stats_in[rr];
+            if (LNM != fh::LN_NONE) sti[tm] = g.stats_in[rr];
         }
     };
     auto epi_store = [&](int ti) {
@@ -235,28 +227,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
 #pragma unroll
         for (int tm = 0; tm < MT; ++tm) {
             const uint32_t row = (uint32_t)(m0 + (wm * MT + tm) * 16 + (lane & 15));
-            f32x2 rs = {0.f, 0.f};
-            if (LNM == fh::LN_IN) {
-                // Chunk sums c0..c7 of the row sit in lane groups 0..3 (ks 0:
-                // chunk g, ks 1: chunk g+4); reduce as ((c0+c1)+(c2+c3)) +
-                // ((c4+c5)+(c6+c7)), gemm.hip's order.
-                float s0 = ssum[0][tm], s1 = ssum[1][tm], q0 = ssq[0][tm], q1 = ssq[1][tm];
-                s0 += __shfl_xor(s0, 16, 64);
-                s1 += __shfl_xor(s1, 16, 64);
-                q0 += __shfl_xor(q0, 16, 64);
-                q1 += __shfl_xor(q1, 16, 64);
-                s0 += __shfl_xor(s0, 32, 64);
-                s1 += __shfl_xor(s1, 32, 64);
-                q0 += __shfl_xor(q0, 32, 64);
-                q1 += __shfl_xor(q1, 32, 64);
-                const float invk = 1.0f / (float)g.K;
-                rs = ln_stats(s0 + s1, q0 + q1, invk, g.ln_eps);
-                // One lane per row of the first column tile writes it; the
-                // others aim past the buffer's range.
-                const bool w = nt == 0 && wn == 0 && lane < 16;
-                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, rs), rS, w ? row * 8u : 0xfffffff0u, 0,
-                                                      0);
-            }
+            const f32x2 rs = LNM != fh::LN_NONE ? sti[tm] : (f32x2){0.f, 0.f};
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 f32x4 v[2];
@@ -275,7 +246,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
                     } else if (RES == 2) {
                         const f16x8 r8 = rh[tm][h];
                         const f16x4 r4 = half ? (f16x4){r8[4], r8[5], r8[6], r8[7]} : (f16x4){r8[0], r8[1], r8[2], r8[3]};
-                        if (LNM == fh::RES_LN) x += ln_resid_v(r4, sti[tm], kg[q], kt[q]);
+                        if (LNM == fh::RES_LN) x += ln_resid_v(r4, rs, kg[q], kt[q]);
                         else x += (f32x4){(float)r4[0], (float)r4[1], (float)r4[2], (float)r4[3]};
                     }
                     v[half] = x;
@@ -297,30 +268,34 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
         }
     };
     // Vector memory instructions epi_store issues after its loads.
-    constexpr int NSTORE = MT * (OUT_F32 ? 4 : 2) + (LNM == fh::LN_IN ? MT : 0);
+    constexpr int NSTORE = MT * (OUT_F32 ? 4 : 2);
 
-    // Ring: slice s lives in slot s % 3; two slices are in flight while one
-    // is multiplied.  Before multiplying slice s this wave waits until slice
-    // s's DMA has landed, then the barrier makes every wave's part of slice s
-    // visible and frees the slot slice s-1 used, for slice s+2.  Vector memory
-    // operations retire in order, so "slice s landed" is "at most n younger
-    // operations outstanding".  Issued after slice s's DMA: slice s+1's DMA
-    // (DPW), and the NSTORE stores of an epilogue that ended slice s−1 or
-    // s−2 (its loads have been consumed, so they are not outstanding).
-    // Counting more than were issued would not wait long enough: n counts at
-    // most one epilogue.
-    issue(0);
-    issue(1);
+    // Ring: slice s lives in slot s % SLOTS; SLOTS−1 slices are in flight
+    // while one is multiplied.  Before multiplying slice s this wave waits
+    // until slice s's DMA has landed, then the barrier makes every wave's
+    // part of slice s visible and frees the slot slice s−1 used, for slice
+    // s+SLOTS−1.  Vector memory operations retire in order, so "slice s
+    // landed" is "at most n younger operations outstanding".  Issued after
+    // slice s's DMA (at iteration s−SLOTS+1): the DMA of slices s+1 ..
+    // s+SLOTS−2, and the NSTORE stores of an epilogue that ended one of
+    // slices s−SLOTS+1 .. s−1 (its loads have been consumed, so they are
+    // not outstanding).  Counting more than were issued would not wait long
+    // enough: n counts at most one epilogue.
+    constexpr int NIN = (SLOTS - 2) * DPW;
+#pragma unroll
+    for (int i = 0; i < SLOTS - 1; ++i) issue(i);
     for (int s = 0; s < nsl; ++s) {
-        const int ks = s % nk;
-        if (s >= 1 && (ks == 0 || (ks == 1 && s >= 2))) {
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPW + NSTORE) : "memory");
+        bool after_epi = false;
+#pragma unroll
+        for (int jj = 1; jj < SLOTS; ++jj) after_epi |= s >= jj && (s - jj + 1) % nk == 0;
+        if (after_epi) {
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NIN + NSTORE) : "memory");
         } else {
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPW) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NIN) : "memory");
         }
         const bool tile_end = (s + 1) % nk == 0;
         if (tile_end) epi_load(s / nk);
-        issue(s + 2);
+        issue(s + SLOTS - 1);
         compute(s % SLOTS);
         if (tile_end) {
             epi_store(s / nk);
@@ -331,7 +306,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1))) void ri
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     static int ncu = 0;
     if (ncu == 0) {
@@ -341,29 +316,61 @@ hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
         ncu = p.multiProcessorCount;
     }
     const int ntn = g.N / BN;
-    const long ntiles = (long)((g.M + BM - 1) / BM) * ntn;
-    // A multiple of 8 blocks (whole XCD groups), at most one per CU.
-    const int cap = (ncu / 8) * 8;
-    const int grid = (int)std::min<long>(cap, (ntiles + 7) / 8 * 8);
+    const long ntiles = (long)((g.M + R::BM - 1) / R::BM) * ntn;
+    // A multiple of 8 blocks (whole XCD groups); persistent: as many as the
+    // CUs hold at once.
+    const long all = (ntiles + 7) / 8 * 8;
+    const int grid = (int)(R::PERSIST ? std::min<long>((long)(ncu / 8) * 8 * R::BPC, all) : all);
     const int per_xcd = (int)((ntiles + 7) / 8);
-    hipLaunchKernelGGL((ring_kernel<ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(NT), 0, s, g, ntn, per_xcd);
+    hipLaunchKernelGGL((ring_kernel<R, ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(R::NT), 0, s, g, ntn, per_xcd);
     return hipGetLastError();
 }
 
 // Selects the kernel for g's bias and residual pointers.
-template <int ACT, bool OUT_F32, int LNM>
-hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+template <class R, int ACT, bool OUT_F32, int LNM>
+hipError_t launch_ring_r(const GemmArgs &g, hipStream_t s) {
     const int res = g.resid ? 1 : g.resid_h ? 2 : 0;
     if (ACT == fh::ACT_RES16 || LNM == fh::RES_LN) {  // binary16 residual by construction
-        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 2>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 2>(g, s);
+        return g.bias ? launch_ring<R, ACT, OUT_F32, LNM, true, 2>(g, s) : launch_ring<R, ACT, OUT_F32, LNM, false, 2>(g, s);
     }
     if (LNM == fh::LN_IN || res == 0) {
-        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 0>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 0>(g, s);
+        return g.bias ? launch_ring<R, ACT, OUT_F32, LNM, true, 0>(g, s) : launch_ring<R, ACT, OUT_F32, LNM, false, 0>(g, s);
     }
     if (res == 1) {
-        return g.bias ? launch_ring<ACT, OUT_F32, LNM, true, 1>(g, s) : launch_ring<ACT, OUT_F32, LNM, false, 1>(g, s);
+        return g.bias ? launch_ring<R, ACT, OUT_F32, LNM, true, 1>(g, s) : launch_ring<R, ACT, OUT_F32, LNM, false, 1>(g, s);
     }
     return hipErrorInvalidValue;  // a binary16 residual outside ACT_RES16
+}
+
+// Configurations (measured on the 18k-token bge-small projections, op level:
+// R0 30.2 µs for QKV, R1 27.8, R2 25.0, R3 32.9, R4 32.7).  The default, R2,
+// runs two persistent 4-wave blocks per CU: while one block waits at its
+// barrier or runs its epilogue, the other keeps the matrix cores busy.
+using R0 = RCfg<256, 128, 4, 2, 3, true>;   // 8 waves, 3 slots, one persistent block per CU
+using R1 = RCfg<128, 128, 2, 2, 2, false>;  // 4 waves, 2 slots, one block per tile (two per CU)
+using R2 = RCfg<128, 128, 2, 2, 2, true>;   // R1's blocks, persistent, two per CU
+using R3 = RCfg<128, 128, 4, 2, 3, true>;   // 8 waves of 32×64, 3 slots, persistent
+using R4 = RCfg<256, 128, 4, 2, 3, false>;  // R0's tile, one block per tile
+
+// FUTON_RING_CFG=0..4 picks a configuration (tuning knob; default 2).
+int ring_cfg() {
+    static const int v = [] {
+        const char *e = getenv("FUTON_RING_CFG");
+        const int c = e ? atoi(e) : 2;
+        return c >= 0 && c <= 4 ? c : 2;
+    }();
+    return v;
+}
+
+template <int ACT, bool OUT_F32, int LNM>
+hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+    switch (ring_cfg()) {
+    case 0: return launch_ring_r<R0, ACT, OUT_F32, LNM>(g, s);
+    case 1: return launch_ring_r<R1, ACT, OUT_F32, LNM>(g, s);
+    case 3: return launch_ring_r<R3, ACT, OUT_F32, LNM>(g, s);
+    case 4: return launch_ring_r<R4, ACT, OUT_F32, LNM>(g, s);
+    default: return launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
+    }
 }
 
 // out row r ← B row ring_pack_row(r), 16 bytes per thread.
@@ -385,6 +392,11 @@ hipError_t ring_pack(const f16 *B, f16 *out, int N, int K, hipStream_t s) {
     return hipGetLastError();
 }
 
+bool gemm_ring_worth(int M, int N) {
+    // Enough 128×128 tiles for about half of the two-per-CU block slots.
+    return N % BN == 0 && (long)((M + 127) / 128) * (N / BN) >= 192;
+}
+
 bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
     if (g.M <= 0 || g.N % BN != 0 || g.K % 64 != 0 || g.K <= 0) return false;
     if (act != ACT_NONE && act != ACT_GELU && act != ACT_RES16) return false;
@@ -394,8 +406,8 @@ bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
     if (act != ACT_RES16 && ln != RES_LN && g.resid_h && !g.resid) return false;
     if (ln == RES_LN && (out_f32 || !g.resid_h || g.resid)) return false;
     // 32-bit buffer offsets: every row the ring addresses (up to M + BM − 1).
-    if (((double)g.M + BM) * g.lda * 2.0 >= 2147483648.0 || (double)g.N * g.ldb * 2.0 >= 2147483648.0) return false;
-    if (((double)g.M + BM) * g.ldc * (out_f32 ? 4.0 : 2.0) >= 2147483648.0) return false;
+    if (((double)g.M + BM_MAX) * g.lda * 2.0 >= 2147483648.0 || (double)g.N * g.ldb * 2.0 >= 2147483648.0) return false;
+    if (((double)g.M + BM_MAX) * g.ldc * (out_f32 ? 4.0 : 2.0) >= 2147483648.0) return false;
     return true;
 }
 

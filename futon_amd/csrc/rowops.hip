@@ -106,9 +106,6 @@ __global__ void gather_rows_kernel(const float *x32, const f16 *x16, const f32x2
     }
 }
 
-// Per-row absmax int8 quantization of activations — native/quant.go:42-70:
-// scale = amax/127 (float32), code = round-half-away(float64(v)·(127/float64(amax))),
-// clamped to ±127; an all-zero row gets scale 0 and zero codes.
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *x, int M, int K, int ldx,
                                                             int8_t *q, float *scale) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -227,6 +224,52 @@ __device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL]
 #pragma unroll
     for (int j = 0; j < VPL; ++j) v[j] = (v[j] - mean) * inv * gw[j] + gb[j];
     st_row<VPL>(o32, o16, lane, v);
+}
+
+// Sum over each 16-lane DPP row (xor 1, xor 2, half-row mirror, row mirror:
+// the row total lands in all 16 lanes), in float64 as two 32-bit halves.
+template <int CTRL>
+__device__ __forceinline__ double dpp_step_f64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)__double2loint(v), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)__double2hiint(v), CTRL, 0xF, 0xF, false);
+    return v + __hiloint2double(hi, lo);
+}
+__device__ __forceinline__ double row16_sum_f64(double v) {
+    v = dpp_step_f64<0xB1>(v);
+    v = dpp_step_f64<0x4E>(v);
+    v = dpp_step_f64<0x141>(v);
+    return dpp_step_f64<0x140>(v);
+}
+
+// (mean, rstd) per row of binary16 y [M, 128·C]: 16 lanes per row, C
+// 16-byte chunks per lane, four rows per wave.  Σy and Σy² in float64
+// (Σy exact for binary16 data), mean = Σy/H, var = Σy²/H − mean² in float64,
+// then float32(mean) and float32(1/sqrt(var + eps)): layerNormRows'
+// (native/model.go:741-770) float64 statistics, for the folded GEMMs.
+template <int C>
+__global__ __launch_bounds__(256) void row_stats_kernel(const f16 *y, int M, float eps, f32x2 *st) {
+    constexpr int H = 128 * C;
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const int r = min(row, M - 1);
+    const int l16 = lane & 15;
+    f16x8 v[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) v[c] = *(const f16x8 *)(y + (size_t)r * H + (c * 16 + l16) * 8);
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const double x = (double)(float)v[c][e];
+            s1 += x;
+            s2 = fma(x, x, s2);
+        }
+    s1 = row16_sum_f64(s1);
+    s2 = row16_sum_f64(s2);
+    const double mean = s1 / H;
+    const double var = fmax(s2 / H - mean * mean, 0.0);
+    if (l16 == 0 && row < M) st[row] = (f32x2){(float)mean, (float)(1.0 / sqrt(var + (double)eps))};
 }
 
 // Two rows per wave: both rows and γ/β are requested before any reduction,
@@ -393,6 +436,19 @@ hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const floa
     if (y16) hipLaunchKernelGGL(layer_norm_kernel<f16>, grid, dim3(256), 0, s, y16, M, H, gamma, beta, eps, x32, x16);
     else hipLaunchKernelGGL(layer_norm_kernel<float>, grid, dim3(256), 0, s, y32, M, H, gamma, beta, eps, x32, x16);
     return hipGetLastError();
+}
+hipError_t row_stats(const f16 *y, int M, int H, float eps, f32x2 *st, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const dim3 grid((M + 15) / 16);
+#define FH_RS_C(C)                                                                                  \
+    case 128 * C: hipLaunchKernelGGL(row_stats_kernel<C>, grid, dim3(256), 0, s, y, M, eps, st); \
+        return hipGetLastError();
+    switch (H) {
+        FH_RS_C(2) FH_RS_C(3) FH_RS_C(4) FH_RS_C(6) FH_RS_C(8)
+    default: break;
+    }
+#undef FH_RS_C
+    return hipErrorInvalidValue;
 }
 hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const int32_t *offsets, int nseq, int H,
                        float *xc32, f16 *xc16, f32x2 *stc, hipStream_t s) {

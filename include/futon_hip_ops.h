@@ -44,18 +44,23 @@ int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, cons
                     void *C, int32_t M, int32_t N, int32_t K, int32_t act, int32_t out_f32, void *stream);
 
 /* The folded-LayerNorm forms of the binary16 GEMM (K % 64 == 0), on the
- * tiled kernel (ring = 0, B as is) or the ring kernel (ring = 1, B packed):
- *  ln_mode 1 (LN_IN):  C = act(rstd·(A·Bᵀ − mean·c1) + c2), (mean, rstd) of
- *                      A's rows (eps) to stats_out [M] float pairs if set;
- *                      act NONE or GELU.
+ * tiled kernel (ring = 0, B as is) or the ring kernel (ring = 1, B packed);
+ * stats holds [M] (mean, rstd) float pairs (fh_op_row_stats):
+ *  ln_mode 1 (LN_IN):  C = act(rstd·(A·Bᵀ − mean·c1) + c2) with A's row
+ *                      statistics; act NONE or GELU.
  *  ln_mode 2 (RES_LN): C = A·Bᵀ + bias + (resid_h − mean)·rstd·ln_g + ln_b
- *                      with (mean, rstd) from stats_in, rounded once.
+ *                      with resid_h's row statistics, rounded once.
  * C is binary16 [M, N].  These are the model's LayerNorm folds of
  * native/model.go:555-633 (LN(x)·Wᵀ and the residual LN). */
 int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const void *B, const float *c1, const float *c2,
-                  void *stats_out, float eps, const float *bias, const void *resid_h, const void *stats_in,
-                  const float *ln_g, const float *ln_b, void *C, int32_t M, int32_t N, int32_t K, int32_t act,
-                  void *stream);
+                  const float *bias, const void *resid_h, const void *stats, const float *ln_g, const float *ln_b,
+                  void *C, int32_t M, int32_t N, int32_t K, int32_t act, void *stream);
+
+/* Per-row LayerNorm statistics of binary16 y [M, H] (H in 256, 384, 512,
+ * 768, 1024): stats[r] = (mean, 1/sqrt(var + eps)) from float64 Σy and Σy²,
+ * rounded to float32 — the float64 statistics of layerNormRows
+ * (native/model.go:741-770) — for the folded GEMMs. */
+int fh_op_row_stats(const void *y, int32_t M, int32_t H, float eps, void *stats, void *stream);
 
 /* Row permutation of a binary16 [N, K] weight matrix (N % 64 == 0, K % 8 == 0)
  * into the order fh_op_gemm_ring reads: inside each 64-row block, packed row

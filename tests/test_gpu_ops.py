@@ -141,48 +141,82 @@ def test_gemm_ring_equals_tiled(M, N, K):
     np.testing.assert_allclose(gemm_ring(da, bp, dbias), ref, atol=2e-4 * math.sqrt(K), rtol=1e-5)
 
 
-def gemm_ln(ring, mode, A, B, C, act=0, c1=None, c2=None, stats=None, eps=1e-12, bias=None, yr=None, st_in=None,
-            lg=None, lb=None):
+def gemm_ln(ring, mode, A, B, C, stats, act=0, c1=None, c2=None, bias=None, yr=None, lg=None, lb=None):
     M, K = A.shape
     N = B.shape[0]
-    rc = _lib().fh_op_gemm_ln(ring, mode, ptr(A), ptr(B), ptr(c1), ptr(c2), ptr(stats), eps, ptr(bias), ptr(yr),
-                              ptr(st_in), ptr(lg), ptr(lb), ptr(C), M, N, K, act, None)
+    rc = _lib().fh_op_gemm_ln(ring, mode, ptr(A), ptr(B), ptr(c1), ptr(c2), ptr(bias), ptr(yr), ptr(stats),
+                              ptr(lg), ptr(lb), ptr(C), M, N, K, act, None)
     assert rc == 0
     sync()
     return C.cpu().numpy()
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 384, 384), (1030, 1536, 384), (257, 384, 1536), (600, 1152, 384)])
-def test_gemm_ln_modes(M, N, K):
-    """The folded-LayerNorm GEMM forms: LN_IN (row statistics of A gathered
-    in the K loop, C = act(rstd·(A·Bᵀ − mean·c1) + c2)) and RES_LN (the
-    residual's LayerNorm rebuilt in the epilogue), on both kernels: the same
-    bits from each, within float tolerance of a float64 restatement."""
-    rng = np.random.default_rng(M + 3 * N + K)
-    y = (rng.standard_normal((M, K)) * 3 + 1.5).astype(np.float16)
-    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
-    c1 = w.astype(np.float64).sum(1).astype(np.float32)
-    c2 = rng.standard_normal(N).astype(np.float32)
-    dy, dw = dev(y), dev(w)
-    wp = torch.empty_like(dw)
-    assert _lib().fh_op_ring_pack(ptr(dw), ptr(wp), N, K, None) == 0
+ROW_STATS_WIDTHS = (256, 384, 512, 768, 1024)
+
+
+def row_stats(y, eps):
+    M, H = y.shape
+    st = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+    assert _lib().fh_op_row_stats(ptr(y), M, H, eps, ptr(st), None) == 0
+    sync()
+    return st
+
+
+def stats64(y, eps):
     y64 = y.astype(np.float64)
     mean = y64.mean(1)
-    rstd = 1.0 / np.sqrt(y64.var(1) + 1e-5)
-    dot = y64 @ w.astype(np.float64).T
+    return mean, 1.0 / np.sqrt(y64.var(1) + eps)
+
+
+@pytest.mark.parametrize("M,H", [(1, 256), (7, 384), (1000, 384), (333, 512), (64, 768), (129, 1024)])
+def test_row_stats_matches_float64(M, H):
+    """Row statistics of binary16 rows: float64 Σy and Σy², rounded to
+    float32 (mean, 1/sqrt(var + eps)) — the float64 statistics of
+    layerNormRows (native/model.go:741-770) — against float64 two-pass
+    statistics, including a row with a large mean and small spread and a
+    constant row (variance 0: rstd = 1/sqrt(eps))."""
+    rng = np.random.default_rng(M + H)
+    y = (rng.standard_normal((M, H)) * 2 + 0.5).astype(np.float16)
+    y[0] = (100 + 0.01 * rng.standard_normal(H)).astype(np.float16)
+    if M > 1:
+        y[1] = np.float16(3.0)
+    eps = 1e-12 if H == 384 else 1e-5
+    st = row_stats(dev(y), eps).cpu().numpy().astype(np.float64)
+    mean, rstd = stats64(y, eps)
+    np.testing.assert_allclose(st[:, 0], mean, rtol=1e-7, atol=1e-9)
+    np.testing.assert_allclose(st[:, 1], rstd, rtol=1e-6)
+    if M > 1:
+        assert st[1, 0] == 3.0 and st[1, 1] == np.float32(1.0 / math.sqrt(float(np.float32(eps))))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 384, 384), (1030, 1536, 384), (257, 384, 768), (600, 1152, 384),
+                                   (12288, 1152, 384), (12288, 384, 1536)])
+def test_gemm_ln_modes(M, N, K):
+    """The folded-LayerNorm GEMM forms: LN_IN (C = act(rstd·(A·Bᵀ − mean·c1)
+    + c2) with A's row statistics) and RES_LN (the residual's LayerNorm
+    rebuilt in the epilogue), on both kernels: the same bits from each,
+    within float tolerance of a float64 restatement."""
+    rng = np.random.default_rng(M + 3 * N + K)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    dw = dev(w)
+    wp = torch.empty_like(dw)
+    assert _lib().fh_op_ring_pack(ptr(dw), ptr(wp), N, K, None) == 0
+    y = (rng.standard_normal((M, K)) * 3 + 1.5).astype(np.float16)
+    c1 = w.astype(np.float64).sum(1).astype(np.float32)
+    c2 = rng.standard_normal(N).astype(np.float32)
+    dy, dc1, dc2 = dev(y), dev(c1), dev(c2)
+    if K in ROW_STATS_WIDTHS:
+        st = row_stats(dy, 1e-5)
+    else:
+        st = dev(np.stack(stats64(y, 1e-5), 1).astype(np.float32))
+    mean, rstd = st.cpu().numpy().astype(np.float64).T
+    dot = y.astype(np.float64) @ w.astype(np.float64).T
     for act in (0, 1):
-        outs, stats = [], []
+        outs = []
         for ring, b in ((0, dw), (1, wp)):
             C = torch.empty((M, N), dtype=torch.float16, device="cuda")
-            st = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
-            outs.append(gemm_ln(ring, 1, dy, b, C, act, dev(c1), dev(c2), st, 1e-5))
-            stats.append(st.cpu().numpy())
-        assert np.array_equal(stats[0], stats[1]), ("stats", np.abs(stats[0] - stats[1]).max(0),
-                                                     int((stats[0] != stats[1]).any(1).sum()))
-        assert np.array_equal(outs[0], outs[1]), ("LN_IN", act, np.abs(outs[0].astype(np.float64) - outs[1]).max(),
-                                                  int((outs[0] != outs[1]).sum()))
-        np.testing.assert_allclose(stats[1][:, 0], mean, atol=1e-5, rtol=1e-5)
-        np.testing.assert_allclose(stats[1][:, 1], rstd, rtol=1e-4)
+            outs.append(gemm_ln(ring, 1, dy, b, C, st, act, dc1, dc2))
+        assert np.array_equal(outs[0], outs[1]), ("LN_IN", act, np.abs(outs[0].astype(np.float64) - outs[1]).max())
         ref = rstd[:, None] * (dot - mean[:, None] * c1) + c2
         if act:
             ref = gelu64(ref)
@@ -190,18 +224,18 @@ def test_gemm_ln_modes(M, N, K):
     a = rng.standard_normal((M, K)).astype(np.float16)
     bias = rng.standard_normal(N).astype(np.float32)
     yr = (rng.standard_normal((M, N)) * 2 + 0.5).astype(np.float16)
-    yr64 = yr.astype(np.float64)
-    st_in = np.stack([yr64.mean(1), 1.0 / np.sqrt(yr64.var(1) + 1e-5)], 1).astype(np.float32)
     lg = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
     lb = (0.1 * rng.standard_normal(N)).astype(np.float32)
-    da, dyr, dst, dlg, dlb, dbias = dev(a), dev(yr), dev(st_in), dev(lg), dev(lb), dev(bias)
+    da, dyr, dlg, dlb, dbias = dev(a), dev(yr), dev(lg), dev(lb), dev(bias)
+    sr = dev(np.stack(stats64(yr, 1e-5), 1).astype(np.float32))
     outs = []
     for ring, b in ((0, dw), (1, wp)):
         C = torch.empty((M, N), dtype=torch.float16, device="cuda")
-        outs.append(gemm_ln(ring, 2, da, b, C, 0, bias=dbias, yr=dyr, st_in=dst, lg=dlg, lb=dlb))
+        outs.append(gemm_ln(ring, 2, da, b, C, sr, bias=dbias, yr=dyr, lg=dlg, lb=dlb))
     assert np.array_equal(outs[0], outs[1]), ("RES_LN", np.abs(outs[0].astype(np.float64) - outs[1]).max())
-    st64 = st_in.astype(np.float64)
-    ref = a.astype(np.float64) @ w.astype(np.float64).T + bias + (yr64 - st64[:, :1]) * st64[:, 1:] * lg + lb
+    mean, rstd = sr.cpu().numpy().astype(np.float64).T
+    ref = (a.astype(np.float64) @ w.astype(np.float64).T + bias +
+           (yr.astype(np.float64) - mean[:, None]) * rstd[:, None] * lg + lb)
     np.testing.assert_allclose(outs[1].astype(np.float64), ref, atol=2e-4 * math.sqrt(K) + 4e-3, rtol=1e-3)
 
 
