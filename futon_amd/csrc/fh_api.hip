@@ -108,6 +108,7 @@ struct DevMat {
     float *scale = nullptr;  // i8: [n]
     int n = 0, k = 0;
     void *wr = nullptr;      // f16 copy with rows in fh::ring_pack_row order for fh::gemm_ring, or null
+    void *wm = nullptr;      // f16 fragment-ordered copy for fh::mlp (fc1: mlp_w1_unit, fc2: mlp_w2_unit), or null
 };
 
 // The persistent ring GEMM pays off once its tiles cover about half the
@@ -129,11 +130,13 @@ enum KClass {
     K_EMBED, K_GEMM_QKV, K_ATTN, K_GEMM_OUT, K_LN, K_GEMM_FFN1, K_GEMM_FC2, K_QUANT, K_GATHER, K_POOL,
     K_CLS_TAIL,  // last CLS layer after its QKV GEMM: attention for row 0 and every M = nseq launch
     K_STATS,     // row statistics for the folded LayerNorms
+    K_MLP,       // fused FFN1 → GELU → FC2 (fh::mlp)
     K_NCLASS
 };
 const char *kClassNames[K_NCLASS] = {"embed_ln",  "gemm_qkv", "attention", "gemm_out",
                                      "layer_norm", "gemm_ffn1", "gemm_fc2", "quantize_rows",
-                                     "gather_cls", "pool_l2",    "cls_last_layer", "row_stats"};
+                                     "gather_cls", "pool_l2",    "cls_last_layer", "row_stats",
+                                     "mlp_fused"};
 
 struct ProfPending {
     int cls;
@@ -320,10 +323,23 @@ void fold_ln(std::vector<float> &w, int n, int k, const std::vector<float> &g, c
 }
 
 // Uploads an [n,k] float matrix as f16 (RNE) or as Q8 codes + scales; with
-// ring, also as f16 rows in fh::ring_pack_row order for fh::gemm_ring.
-int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8, bool ring = false) {
+// ring, also as f16 rows in fh::ring_pack_row order for fh::gemm_ring; with
+// mlp_kind 1 or 2, also as the fragment-ordered fc1 or fc2 copy for fh::mlp.
+int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k, bool q8, bool ring = false,
+               int mlp_kind = 0) {
     d.n = n;
     d.k = k;
+    if (mlp_kind && !q8) {
+        std::vector<uint16_t> h(w.size());
+        for (long u = 0; u < (long)n * k / 8; u++) {
+            int row, col;
+            if (mlp_kind == 1) fh::mlp_w1_unit(u, k, row, col);
+            else fh::mlp_w2_unit(u, row, col);
+            for (int e = 0; e < 8; e++) h[(size_t)u * 8 + e] = f32_to_f16(w[(size_t)row * k + col + e]);
+        }
+        const int rc = upload(m, (uint16_t **)&d.wm, h.data(), h.size() * 2);
+        if (rc) return rc;
+    }
     if (ring && !q8) {
         std::vector<uint16_t> h(w.size());
         for (int r = 0; r < n; r++) {
@@ -545,6 +561,36 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     return FH_OK;
 }
 
+// Whether layer L's feed-forward block runs fused for M rows: its fc2 copy
+// for fh::mlp exists and M is large enough for the ring-sized path.
+bool use_mlp(const DevLayer &L, int M, int I) {
+    return L.fc2.wm && L.ffn1.wm && fh::gemm_ring_worth(M, I) && fh::mlp_ok(M, L.fc2.n, I);
+}
+
+// Fused FFN1 → GELU → FC2 with both LayerNorm folds (fh::mlp):
+// out = GELU(LN1(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN1(y), LN1 from y's statistics.
+int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, const f32x2 *stats, int M, f16 *out, hipStream_t s) {
+    const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
+    MlpArgs g{};
+    g.y = y;
+    g.stats = stats;
+    g.w1 = (const f16 *)L.ffn1.wm;
+    g.c1 = L.ffn1_c1;
+    g.c2 = L.ffn1_c2;
+    g.w2 = (const f16 *)L.fc2.wm;
+    g.b2 = L.fc2_b;
+    g.ln_g = L.n1w;
+    g.ln_b = L.n1b;
+    g.out = out;
+    g.M = M;
+    g.I = I;
+    const double flops = 4.0 * M * (double)H * I;
+    const double bytes = (double)M * H * 2 * 2 + 2.0 * H * I * 2 + M * 8.0;
+    Scope sc(m, K_MLP, flops, bytes, s);
+    LCHK(fh::mlp(g, s));
+    return FH_OK;
+}
+
 // Binary16 GEMM with the residual LN(yr) rebuilt in the epilogue (RES_LN):
 // C = f16(A·Wᵀ + bias + (yr − mean)·rstd·γ + β), yr's statistics from
 // row_stats.
@@ -658,6 +704,10 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // h = act(LN1(yB)·W1ᵀ + b1); yA = h·W2ᵀ + b2 + LN1(yB)  (model.go:607-633)
+        if (use_mlp(L, M, I)) {
+            if ((rc = row_stats(m, K_STATS, yBo, M, sB, s)) || (rc = mlp_fused(m, L, yBo, sB, M, yA, s))) return rc;
+            continue;
+        }
         if ((rc = row_stats(m, last_cls ? K_CLS_TAIL : K_STATS, yBo, M, sB, s)) ||
             (rc = gemm_lnin(m, kFfn1, L.ffn1, yBo, M, L.ffn1_c1, L.ffn1_c2, sB, m->hbuf, I,
                             swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU, s)))
@@ -882,6 +932,11 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     const char *ring_env = getenv("FUTON_GEMM_RING");
     const bool ring_on = m->lnfold && !(ring_env && ring_env[0] == '0');
     auto ring_fits = [&](int n, int k) { return ring_on && n % 128 == 0 && k % 64 == 0; };
+    // The feed-forward block runs fused (fh::mlp) for hidden width 384 with
+    // GELU; FUTON_MLP=0 keeps the two ring GEMMs (diagnostics).
+    const char *mlp_env = getenv("FUTON_MLP");
+    const bool mlp_on = ring_on && !swiglu && !(mlp_env && mlp_env[0] == '0') && fh::mlp_ok(1, H, I) &&
+                        ring_fits(I, H);
     std::vector<float> gA, bA, g1, b1, bias, c1, c2;
     if (m->lnfold && ((rc = ld.vec_host("embeddings.norm.weight", H, gA)) ||
                       (rc = ld.vec_host("embeddings.norm.bias", H, bA))))
@@ -947,11 +1002,11 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                     (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
                     return bail(rc);
             }
-            if ((rc = upload_mat(m, L.ffn1, w, I, H, q8, ring_fits(I, H)))) return bail(rc);
+            if ((rc = upload_mat(m, L.ffn1, w, I, H, q8, ring_fits(I, H), mlp_on ? 1 : 0))) return bail(rc);
             if ((rc = ld.vec_f32(nm("mlp.fc1.bias"), I, &L.ffn1_b, true))) return bail(rc);
         }
         if ((rc = ld.mat_host(nm("mlp.fc2.weight"), H, I, w)) ||
-            (rc = upload_mat(m, L.fc2, w, H, I, q8, ring_fits(H, I))))
+            (rc = upload_mat(m, L.fc2, w, H, I, q8, ring_fits(H, I), mlp_on ? 2 : 0)))
             return bail(rc);
         if ((rc = ld.vec_f32(nm("mlp.fc2.bias"), H, &L.fc2_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm2.weight"), H, &L.n2w)) || (rc = ld.vec_f32(nm("norm2.bias"), H, &L.n2b)))

@@ -46,6 +46,20 @@ struct GemmArgs {
     const float *ln_g, *ln_b;   // RES_LN: γ, β of resid_h's LayerNorm
 };
 
+// Fused feed-forward block (mlp.hip), hidden width 384:
+// out = GELU(rstd·(y·W1ᵀ − mean·c1) + c2)·W2ᵀ + b2 + ((y − mean)·rstd·γ + β).
+struct MlpArgs {
+    const f16 *y;              // [M, 384] un-normalized LayerNorm input
+    const f32x2 *stats;        // [M] (mean, rstd) of y's rows
+    const f16 *w1;             // fc1 weights [I, 384] scaled by γ, fragment-ordered (mlp_w1_unit)
+    const float *c1, *c2;      // [I] LayerNorm fold terms of fc1 (c2 includes fc1's bias)
+    const f16 *w2;             // fc2 weights [384, I], fragment-ordered (mlp_w2_unit)
+    const float *b2;           // [384] fc2 bias, or null
+    const float *ln_g, *ln_b;  // [384] γ, β of y's LayerNorm (the residual)
+    f16 *out;                  // [M, 384]
+    int M, I;
+};
+
 struct AttnArgs {
     const f16 *qkv;        // [T, 3H] f16: q | k | v, heads-major inside each
     const int32_t *offsets;  // [nseq + 1] packed sequence starts
@@ -84,6 +98,49 @@ __host__ __device__ inline int ring_pack_row(int r) {
     const int p = r & 63, tn = p >> 4, g = (p >> 2) & 3, e = p & 3;
     return (r & ~63) | ((tn >> 1) * 32 + g * 8 + (tn & 1) * 4 + e);
 }
+// Fragment-ordered weight copies for mlp(): a sequence of 1-KB MFMA operand
+// fragments (16 rows × 32 columns, lane l holding row l%16, columns
+// 8·(l/16) .. +7), ordered the way each of the kernel's MLP_NW waves consumes
+// them.  mlp_w1_unit / mlp_w2_unit give, for 16-byte unit u of the packed
+// copy, the source row and first column of its 8 binary16 values.
+constexpr int MLP_NW = 8;                          // waves per fused block
+constexpr int MLP_NT1 = 128 / MLP_NW / 16;         // fc1 16-row tiles per wave and 128-feature chunk
+constexpr int MLP_NT2 = 384 / MLP_NW / 16;         // fc2 16-row tiles per wave
+// fc1 [I, K]: fragment f = (g·(K/32) + ks)·NT1 + tn for 16·NT1-row group g,
+// k-step ks, tile tn; MFMA row 16tn + 4a + e of a group is its row
+// 4·NT1·a + 4tn + e, so each lane ends with 4·NT1 consecutive features.
+__host__ __device__ inline void mlp_w1_unit(long u, int K, int &row, int &col) {
+    const int l = (int)(u & 63);
+    long f = u >> 6;
+    const int tn = (int)(f % MLP_NT1);
+    f /= MLP_NT1;
+    const int ks = (int)(f % (K / 32)), grp = (int)(f / (K / 32));
+    const int p = 16 * tn + (l & 15);
+    row = grp * 16 * MLP_NT1 + 4 * MLP_NT1 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3);
+    col = ks * 32 + (l >> 4) * 8;
+}
+// fc2 [384, I]: per 128-column chunk j, wave w (16·NT2 output rows), k-step
+// ks, tile t: f = ((j·NW + w)·4 + ks)·NT2 + t; MFMA row 16t + 4a + e of a
+// wave's rows is its row 4·NT2·a + 4t + e, so each lane ends with 4·NT2
+// consecutive outputs.
+__host__ __device__ inline void mlp_w2_unit(long u, int &row, int &col) {
+    const int l = (int)(u & 63);
+    long f = u >> 6;
+    const int t = (int)(f % MLP_NT2);
+    f /= MLP_NT2;
+    const int ks = (int)(f % 4);
+    f /= 4;
+    const int w = (int)(f % MLP_NW), j = (int)(f / MLP_NW);
+    const int p = 16 * t + (l & 15);
+    row = 16 * MLP_NT2 * w + 4 * MLP_NT2 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3);
+    col = j * 128 + ks * 32 + (l >> 4) * 8;
+}
+// out = the fragment-ordered copy of B [N, K]: kind 1 (fc1, K % 32 == 0,
+// N % (16·MLP_NT1) == 0) or kind 2 (fc2, N == 384, K % 128 == 0).
+hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s);
+// Whether mlp() takes an M-row problem with intermediate width I.
+bool mlp_ok(int M, int H, int I);
+hipError_t mlp(const MlpArgs &a, hipStream_t s);
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
 // gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
 // binary16 sum to x16 instead, for a consumer that folds this LayerNorm.

@@ -118,6 +118,34 @@ extern "C" int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, v
     return code_of(fh::ring_pack((const f16 *)B, (f16 *)out, N, K, (hipStream_t)stream));
 }
 
+extern "C" int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N, int32_t K, void *stream) {
+    if (!B || !out || N <= 0 || K <= 0) return FH_EINVAL;
+    if (kind == 1 ? N % 16 || K % 32 : kind != 2 || N != 384 || K % 128) return FH_EINVAL;
+    return code_of(fh::mlp_pack(kind, (const f16 *)B, (f16 *)out, N, K, (hipStream_t)stream));
+}
+
+extern "C" int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const float *c1, const float *c2,
+                         const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
+                         int32_t M, int32_t H, int32_t I, void *stream) {
+    if (!y || !stats || !w1_packed || !c1 || !c2 || !w2_packed || !ln_g || !ln_b || !out || M < 0) return FH_EINVAL;
+    if (M == 0) return FH_OK;
+    if (!fh::mlp_ok(M, H, I)) return FH_EINVAL;
+    MlpArgs g{};
+    g.y = (const f16 *)y;
+    g.stats = (const f32x2 *)stats;
+    g.w1 = (const f16 *)w1_packed;
+    g.c1 = c1;
+    g.c2 = c2;
+    g.w2 = (const f16 *)w2_packed;
+    g.b2 = b2;
+    g.ln_g = ln_g;
+    g.ln_b = ln_b;
+    g.out = (f16 *)out;
+    g.M = M;
+    g.I = I;
+    return code_of(fh::mlp(g, (hipStream_t)stream));
+}
+
 extern "C" int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32_t max_len, int32_t H,
                                int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
                                int32_t q_limit, int32_t compact, int32_t out_f32, void *stream) {

@@ -28,9 +28,12 @@
 
 #include "fh_common.h"
 #include "gemm_epi.h"
+#include "lds_dma.h"
 
 namespace {
 using namespace fh_epi;
+using fh_dma::buf_rsrc;
+using fh_dma::dma16;
 
 constexpr int ROWB = 128;  // bytes of K per slice row (64 f16)
 
@@ -52,20 +55,6 @@ struct RCfg {
 };
 constexpr int BN = 128;     // every configuration's column tile (the packing unit × 2)
 constexpr int BM_MAX = 256;
-
-// Buffer resource for raw loads and stores of `bytes` bytes at p: offsets
-// at or beyond `bytes` read as zero and are not written.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// 16 bytes per lane from rs + voff + soff into LDS at lds_addr + lane·16
-// (buffer_load_dwordx4 … lds).  The ring orders these against its LDS reads
-// itself (s_waitcnt vmcnt + barrier); the compiler counts them in vmcnt.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(uintptr_t)lds_addr, 16,
-                                             voff, soff, 0, 0);
-}
 
 // RES: no residual (0), f32 (1) or binary16 (2); BIAS: g.bias is set.  The
 // epilogue is straight-line code for each combination, so the number of

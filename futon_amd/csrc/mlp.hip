@@ -1,0 +1,332 @@
+// Fused feed-forward block of the encoder layer on gfx950 (hidden width 384):
+//   h   = GELU(LN(y)·W1ᵀ + b1)          (native/model.go:607-620)
+//   out = h·W2ᵀ + b2 + LN(y)           (native/model.go:622-633)
+// with LN(y) folded as in the separate GEMMs (W1 stored scaled by γ, the fold
+// terms c1/c2, y's row statistics from row_stats).  h never leaves the CU: it
+// is produced 128 intermediate features at a time into LDS and consumed there
+// by the second product, which saves the [M, I] binary16 round trip through
+// HBM and one launch per layer.
+//
+// Layout and schedule, one 8-wave block per BM = 16·MT tokens:
+// * The block's token tile y[BM, 384] is DMA'd into LDS once (buffer_load …
+//   lds) and stays resident; rows past M read as zero.  LDS rows are 128
+//   bytes with the 16-byte chunk index XOR-ed with row%8, so MFMA fragment
+//   reads (16 rows × one chunk) are conflict-free.
+// * Weights never pass through LDS: both matrices are stored as 1-KB MFMA
+//   operand fragments in the order each wave consumes them (mlp_w1_unit,
+//   mlp_w2_unit), and every wave loads its own fragments straight into
+//   registers ahead of use (W1 half a chunk, W2 a chunk).  Each weight byte
+//   is read once per block.
+// * v_mfma_f32_16x16x32_f16, weights as the A operand.  Per 128-feature chunk
+//   j, wave w: phase 1 computes features 16w .. 16w+15 for all BM tokens;
+//   its epilogue (LayerNorm fold, GELU, rounding to binary16) writes h into
+//   LDS; after one barrier, phase 2 accumulates outputs 48w .. 48w+47 over
+//   the chunk's 128 features.  h is double-buffered, so that barrier is the
+//   chunk's only one, and each chunk's epilogue (the VALU-heavy part) is
+//   split between the previous chunk's phase 2 and the next chunk's phase 1,
+//   so the matrix and vector units work side by side.  The fold terms c1/c2
+//   are staged in LDS once per block.
+// The accumulation orders over K and the epilogue arithmetic are those of the
+// ring GEMM's LN_IN/GELU and RES_LN forms, so the result has the same bits as
+// the two separate GEMMs.
+#include <algorithm>
+
+#include "fh_common.h"
+#include "gemm_epi.h"
+#include "lds_dma.h"
+
+namespace {
+using namespace fh_epi;
+using fh_dma::buf_rsrc;
+using fh_dma::dma16;
+
+constexpr int HD = 384;                 // hidden width
+constexpr int KB1 = HD / 64;            // 64-wide k-blocks of the token tile
+constexpr int CH = 128;                 // intermediate features per chunk
+constexpr int KS1 = HD / 32;            // phase-1 k-steps per chunk
+constexpr int KS2 = CH / 32;            // phase-2 k-steps per chunk
+constexpr int W1H = KS1 / 2;            // W1 k-steps held in registers
+constexpr int NW = fh::MLP_NW;              // waves per block
+constexpr int NT1 = fh::MLP_NT1;            // phase-1 feature tiles per wave
+constexpr int NT2 = fh::MLP_NT2;            // phase-2 output tiles per wave
+constexpr int ROWB = 128;               // bytes per LDS row (64 binary16)
+constexpr int MT_MAX = 5;
+constexpr int I_MAX = 2048;             // widest intermediate layer (fold terms staged in LDS)
+constexpr int W1C = NW * KS1 * NT1 * 64;  // 16-byte units of W1 per chunk
+constexpr int W2C = NW * KS2 * NT2 * 64;  // 16-byte units of W2 per chunk
+static_assert(CH == NW * 16 * NT1 && NT2 * 16 * NW == HD, "wave split");
+
+template <int MT, bool BIAS>
+__global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
+    constexpr int BM = 16 * MT;
+    constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
+    constexpr int H_BYTES = (CH / 64) * BM * ROWB;  // one chunk's h, k-block major
+    constexpr int C_OFF = A_BYTES + 2 * H_BYTES;    // c1 [I_MAX] then c2 [I_MAX] (f32)
+    constexpr int S_OFF = C_OFF + 2 * I_MAX * 4;    // (mean, rstd) of the tile's rows
+    constexpr int TS = MT;                          // epilogue tiles done beside phase 2 (all)
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S_OFF + BM * 8];
+    const uint8_t *const atile = lds;
+    const float *const lc1 = (const float *)(lds + C_OFF), *const lc2 = lc1 + I_MAX;
+    f32x2 *const lst = (f32x2 *)(lds + S_OFF);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = blockIdx.x * BM;
+    const int nchunk = g.I / CH;
+
+    // This wave's weight fragments of chunk j: W1 (ks, tn), W2 (ks, t).  W1
+    // is held half a chunk ahead: slot ks % W1H holds k-step ks, refilled with
+    // k-step ks + W1H (of the same chunk, or ks − W1H of the next) once
+    // consumed.  W2 is held a whole chunk ahead.
+    const i32x4 *w1p = (const i32x4 *)g.w1 + (size_t)wave * KS1 * NT1 * 64 + lane;
+    const i32x4 *w2p = (const i32x4 *)g.w2 + (size_t)wave * KS2 * NT2 * 64 + lane;
+    i32x4 w1f[W1H][NT1], w2f[KS2][NT2];
+#pragma unroll
+    for (int ks = 0; ks < W1H; ++ks)
+#pragma unroll
+        for (int tn = 0; tn < NT1; ++tn) w1f[ks][tn] = w1p[(ks * NT1 + tn) * 64];
+    // After multiplying k-step ks of chunk c: refill its slot.
+    auto w1_refill = [&](int c, int ks) {
+        const int cc = ks < W1H ? c : min(c + 1, nchunk - 1), kk = ks < W1H ? ks + W1H : ks - W1H;
+#pragma unroll
+        for (int tn = 0; tn < NT1; ++tn) w1f[ks % W1H][tn] = w1p[(size_t)cc * W1C + (kk * NT1 + tn) * 64];
+    };
+#pragma unroll
+    for (int ks = 0; ks < KS2; ++ks)
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) w2f[ks][t] = w2p[(ks * NT2 + t) * 64];
+
+    // Row statistics of the tile's rows (rows past M clamped: never stored).
+    if ((int)threadIdx.x < BM) lst[threadIdx.x] = g.stats[min(m0 + (int)threadIdx.x, g.M - 1)];
+
+    // Into LDS: the token tile (DMA block b = rows 8·(b % 2MT) .. of k-block
+    // b / 2MT; a block is 8 rows, lane l writing physical chunk l%8 of row l/8,
+    // i.e. logical chunk (l%8) ^ (l/8)) and the fold terms c1, c2 (1 KB per
+    // block, lane-linear).  Blocks wave, wave + NW, ...
+    {
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+        const __amdgpu_buffer_rsrc_t rY = buf_rsrc(g.y, (uint32_t)g.M * (HD * 2));
+        const uint32_t lrow = lane >> 3, lchunk = ((lane & 7) ^ (lane >> 3)) * 16;
+#pragma unroll
+        for (int i = 0; i < (12 * MT + NW - 1) / NW; ++i) {
+            const int b = wave + NW * i, kb = b / (2 * MT), rb = b - kb * 2 * MT;
+            if (b < 12 * MT)
+                dma16(rY, lds0 + (uint32_t)b * 1024, (uint32_t)(m0 + rb * 8 + (int)lrow) * (HD * 2) + lchunk,
+                      (uint32_t)kb * ROWB);
+        }
+        const __amdgpu_buffer_rsrc_t rC1 = buf_rsrc(g.c1, (uint32_t)g.I * 4);
+        const __amdgpu_buffer_rsrc_t rC2 = buf_rsrc(g.c2, (uint32_t)g.I * 4);
+        const int ncb = (g.I * 4 + 1023) / 1024;
+        for (int b = wave; b < 2 * ncb; b += NW) {
+            const int which = b >= ncb, kb = b - which * ncb;
+            dma16(which ? rC2 : rC1, lds0 + C_OFF + (uint32_t)which * (I_MAX * 4) + (uint32_t)kb * 1024,
+                  (uint32_t)lane * 16, (uint32_t)kb * 1024);
+        }
+    }
+    // Everything above has landed (the weights were requested first, so
+    // their latency overlaps the tile's) and every wave's part is visible.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // Fragment offsets inside a 16-row group: row lane%16, logical chunk
+    // lane/16 + 4·(ks%2) at physical chunk ^ (lane%8).
+    int fo[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) fo[k] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * k) ^ (lane & 7)) << 4);
+    // Chunk-local phase-1 features of this lane: fl .. fl + 4·NT1 − 1.
+    const int fl = wave * 16 * NT1 + (lane >> 4) * 4 * NT1;
+
+    f32x4 accA[NT1][MT], accB[NT1][MT], acc2[NT2][MT];
+#pragma unroll
+    for (int tm = 0; tm < MT; ++tm)
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) acc2[t][tm] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // Phase 1, k-step ks: acc (+)= W1 fragments · y_tileᵀ (ks 0 starts at 0).
+    auto p1_step = [&](int ks, f32x4(&acc)[NT1][MT]) {
+        const uint8_t *ab = atile + (ks >> 1) * BM * ROWB + fo[ks & 1];
+        i32x4 af[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+#pragma unroll
+        for (int tn = 0; tn < NT1; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < MT; ++tm)
+                acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8, w1f[ks % W1H][tn]), __builtin_bit_cast(f16x8, af[tm]),
+                    ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[tn][tm], 0, 0, 0);
+    };
+    // Phase-1 epilogue of token tile tm of chunk c (acc holds its finished
+    // product): fold, GELU, binary16, into h buffer c % 2 at this lane's
+    // 4·NT1 features.
+    auto epi1_tm = [&](int tm, const f32x4(&acc)[NT1][MT], int c) {
+        const f32x2 sv = lst[tm * 16 + (lane & 15)];
+        _Float16 o[4 * NT1] __attribute__((aligned(16)));
+#pragma unroll
+        for (int tn = 0; tn < NT1; ++tn) {
+            const f32x4 k1 = *(const f32x4 *)(lc1 + c * CH + fl + 4 * tn);
+            const f32x4 k2 = *(const f32x4 *)(lc2 + c * CH + fl + 4 * tn);
+            const f32x4 x = ln_fold_v(acc[tn][tm], sv, k1, k2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[4 * tn + i] = to_f16(gelu_erf(x[i]));
+        }
+        const int row = tm * 16 + (lane & 15);
+        uint8_t *dst = lds + A_BYTES + (c & 1) * H_BYTES + (fl >> 6) * BM * ROWB + row * ROWB +
+                       ((((fl & 63) >> 3) ^ (lane & 7)) << 4) + (fl & 7) * 2;
+        if (NT1 == 2) *(f16x8 *)dst = *(const f16x8 *)o;
+        else *(f16x4 *)dst = *(const f16x4 *)o;
+    };
+
+    // Chunk 0's phase 1 and the first part of its epilogue; its W1 registers
+    // are refilled with chunk 1's fragments.
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+        p1_step(ks, accA);
+        w1_refill(0, ks);
+    }
+#pragma unroll
+    for (int tm = 0; tm < TS; ++tm) epi1_tm(tm, accA, 0);
+
+    // Chunk j: stage A multiplies chunk j+1's phase 1 into accN (refilling
+    // W1 with chunk j+2's fragments) beside the rest of chunk j's epilogue
+    // (accC); one barrier; stage B multiplies chunk j's phase 2 (refilling W2
+    // with chunk j+1's) beside the first part of chunk j+1's epilogue.  h is
+    // double-buffered: chunk j+1's h goes to the buffer chunk j−1 used, read
+    // by every wave before it passed this chunk's barrier.
+    auto chunk = [&](int j, f32x4(&accC)[NT1][MT], f32x4(&accN)[NT1][MT]) {
+        const bool more = j + 1 < nchunk;
+        if (more) {
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks) {
+                p1_step(ks, accN);
+                if (TS + ks < MT) epi1_tm(TS + ks, accC, j);
+                w1_refill(j + 1, ks);
+            }
+        } else {
+#pragma unroll
+            for (int tm = TS; tm < MT; ++tm) epi1_tm(tm, accC, j);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const uint8_t *hb = lds + A_BYTES + (j & 1) * H_BYTES;
+        const size_t next2 = (size_t)min(j + 1, nchunk - 1) * W2C;
+#pragma unroll
+        for (int ks = 0; ks < KS2; ++ks) {
+            const uint8_t *hr = hb + (ks >> 1) * BM * ROWB + fo[ks & 1];
+            i32x4 hf[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) hf[t] = *(const i32x4 *)(hr + t * 16 * ROWB);
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+#pragma unroll
+                for (int tm = 0; tm < MT; ++tm)
+                    acc2[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, w2f[ks][t]), __builtin_bit_cast(f16x8, hf[tm]), acc2[t][tm], 0, 0, 0);
+                w2f[ks][t] = w2p[next2 + (ks * NT2 + t) * 64];
+            }
+            if (more) {
+#pragma unroll
+                for (int tm = ks * TS / KS2; tm < (ks + 1) * TS / KS2; ++tm) epi1_tm(tm, accN, j + 1);
+            }
+        }
+    };
+    for (int j = 0; j < nchunk; j += 2) {
+        chunk(j, accA, accB);
+        if (j + 1 < nchunk) chunk(j + 1, accB, accA);
+    }
+
+    // Output epilogue: acc + b2 + (y − mean)·rstd·γ + β, rounded once; y read
+    // back from the resident token tile.  This lane's outputs:
+    // n0 = 16·NT2·wave + 4·NT2·(lane/16) + {0 .. 4·NT2 − 1}.
+    const __amdgpu_buffer_rsrc_t rO = buf_rsrc(g.out, (uint32_t)g.M * (HD * 2));
+    const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
+    f32x4 kb[NT2], kg[NT2], kt[NT2];
+#pragma unroll
+    for (int t = 0; t < NT2; ++t) {
+        if (BIAS) kb[t] = *(const f32x4 *)(g.b2 + n0 + 4 * t);
+        kg[t] = *(const f32x4 *)(g.ln_g + n0 + 4 * t);
+        kt[t] = *(const f32x4 *)(g.ln_b + n0 + 4 * t);
+    }
+#pragma unroll
+    for (int tm = 0; tm < MT; ++tm) {
+        const int r = tm * 16 + (lane & 15);
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            const int n = n0 + 4 * t;
+            const f16x4 y4 = *(const f16x4 *)(atile + (n >> 6) * BM * ROWB + r * ROWB +
+                                              ((((n & 63) >> 3) ^ (lane & 7)) << 4) + (n & 7) * 2);
+            f32x4 x = acc2[t][tm];
+            if (BIAS) x += kb[t];
+            x += ln_resid_v(y4, lst[r], kg[t], kt[t]);
+            f16x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rO, (uint32_t)((m0 + r) * HD + n) * 2,
+                                                  0, 0);
+        }
+    }
+}
+
+// out = the fragment-ordered copy of B, 16 bytes per thread.
+__global__ void mlp_pack_kernel(int kind, const f16 *__restrict__ B, f16 *__restrict__ out, int N, int K) {
+    const long u = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= (long)N * K / 8) return;
+    int row, col;
+    if (kind == 1) fh::mlp_w1_unit(u, K, row, col);
+    else fh::mlp_w2_unit(u, row, col);
+    *(f16x8 *)(out + u * 8) = *(const f16x8 *)(B + (size_t)row * K + col);
+}
+
+int cu_count() {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+        ncu = p.multiProcessorCount;
+    }
+    return ncu;
+}
+
+template <int MT>
+hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
+    const int grid = (g.M + 16 * MT - 1) / (16 * MT);
+    if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true>), dim3(grid), dim3(64 * NW), 0, s, g);
+    else hipLaunchKernelGGL((mlp_kernel<MT, false>), dim3(grid), dim3(64 * NW), 0, s, g);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+namespace fh {
+
+hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s) {
+    if (N <= 0 || K <= 0 || !(kind == 1 ? N % (16 * NT1) == 0 && K % 32 == 0 : kind == 2 && N == HD && K % CH == 0))
+        return hipErrorInvalidValue;
+    const long n = (long)N * (K / 8);
+    hipLaunchKernelGGL(mlp_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kind, B, out, N, K);
+    return hipGetLastError();
+}
+
+bool mlp_ok(int M, int H, int I) {
+    // 32-bit buffer offsets for y/out (M·768 bytes) and the weights.
+    return H == HD && I > 0 && I % CH == 0 && I <= I_MAX && M > 0 && (double)M * HD * 2 < 2147483648.0 &&
+           (double)I * HD * 2 < 2147483648.0;
+}
+
+hipError_t mlp(const MlpArgs &g, hipStream_t s) {
+    if (!mlp_ok(g.M, HD, g.I) || !g.y || !g.stats || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
+        return hipErrorInvalidValue;
+    const int ncu = cu_count();
+    if (ncu <= 0) return hipErrorUnknown;
+    // Tokens per block: the fewest 16-row tiles that cover M with one block
+    // per CU (weights are re-read once per block, so fewer, larger blocks).
+    const int mt = std::min(MT_MAX, std::max(1, (g.M + 16 * ncu - 1) / (16 * ncu)));
+    switch (mt) {
+    case 1: return launch_mlp<1>(g, s);
+    case 2: return launch_mlp<2>(g, s);
+    case 3: return launch_mlp<3>(g, s);
+    case 4: return launch_mlp<4>(g, s);
+    default: return launch_mlp<5>(g, s);
+    }
+}
+
+}  // namespace fh

@@ -68,6 +68,30 @@ int fh_op_row_stats(const void *y, int32_t M, int32_t H, float eps, void *stats,
  * counterpart (a layout of this build). */
 int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream);
 
+/* Fragment-ordered copy of a binary16 [N, K] weight matrix for fh_op_mlp: a
+ * sequence of 1-KB MFMA operand fragments (16 rows × 32 columns; 16-byte
+ * unit u holds row r, columns c .. c+7 with lane l = u % 64 taking row
+ * l % 16 of its tile and columns 8·(l/16) ..).  kind 1 (fc1 [I, 384], N % 16
+ * == 0, K % 32 == 0): fragment f = u / 64 is 16-row tile f / (K/32), k-step
+ * f % (K/32).  kind 2 (fc2 [384, I], K % 128 == 0): f = ((8j + w)·4 + ks)·3 +
+ * t for 128-column chunk j, 48-row group w, k-step ks, tile t, and MFMA row
+ * 16t + 4g + e of a group is row 12g + 4t + e.  No reference counterpart (a
+ * layout of this build). */
+int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N, int32_t K, void *stream);
+
+/* The encoder layer's feed-forward block in one kernel, hidden width H = 384,
+ * GELU, I % 128 == 0:
+ *   out = GELU(rstd·(y·W1ᵀ − mean·c1) + c2)·W2ᵀ + b2 + (y − mean)·rstd·ln_g + ln_b
+ * y [M, 384] binary16 (un-normalized), stats [M] (mean, rstd) float pairs of
+ * y's rows (fh_op_row_stats), w1_packed = fh_op_mlp_pack kind 1 of W1 [I, 384],
+ * w2_packed = kind 2 of W2 [384, I], b2 may be NULL; out [M, 384]
+ * binary16.  The intermediate GELU output never reaches memory; the result
+ * has the same bits as fh_op_gemm_ln LN_IN + GELU followed by RES_LN.
+ * Replaces: the MLP block of the encoder layer (native/model.go:607-633). */
+int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const float *c1, const float *c2,
+              const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out, int32_t M,
+              int32_t H, int32_t I, void *stream);
+
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,
  * holding each sequence's first q_limit=1 query row), f32 or binary16.

@@ -184,3 +184,27 @@ def test_ring_gemm_forward_equals_tiled(name, batch, monkeypatch):
     assert np.array_equal(a, b), np.abs(a - b).max()
     ring.close()
     tiled.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192)])
+def test_fused_mlp_forward_equals_two_gemms(name, batch, monkeypatch):
+    """At hidden width 384 the feed-forward block runs as one fused kernel
+    (the default at these 12k-13k token batches); the forward returns the
+    same bits as with the block's two ring GEMMs (FUTON_MLP=0)."""
+    w = synth.workload(name)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    ids, offsets = synth.make_batch(w.ids_seed + 9, batch, w.len_lo, w.len_hi)
+    native = _native()
+    fused = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    monkeypatch.setenv("FUTON_MLP", "0")
+    split = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    fused.profile_reset()
+    fused.profile_enable(True)
+    a = fused.EncodePacked(ids, offsets, w.out_dim)
+    fused.profile_enable(False)
+    assert fused.profile_read()["mlp_fused"]["launches"] > 0
+    b = split.EncodePacked(ids, offsets, w.out_dim)
+    assert np.array_equal(a, b), np.abs(a - b).max()
+    fused.close()
+    split.close()

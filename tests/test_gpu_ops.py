@@ -249,6 +249,101 @@ def test_gemm_ring_rejects_unfit_shapes():
     assert _lib().fh_op_gemm_ring(ptr(d), ptr(d), None, None, 0, ptr(c), 8, 128, 64, 2, 1, None) == lib.FH_EINVAL
 
 
+def mlp_units(kind, N, K):
+    """(row, col) of each 16-byte unit of the fh_op_mlp_pack copy, restated
+    from its documented layout."""
+    u = np.arange(N * K // 8)
+    lane, f = u % 64, u // 64
+    if kind == 1:
+        return (f // (K // 32)) * 16 + lane % 16, (f % (K // 32)) * 32 + (lane // 16) * 8
+    t, f = f % 3, f // 3
+    ks, f = f % 4, f // 4
+    w, j = f % 8, f // 8
+    p = 16 * t + lane % 16
+    return 48 * w + 12 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3), j * 128 + ks * 32 + (lane // 16) * 8
+
+
+def mlp_pack(kind, d):
+    out = torch.empty_like(d)
+    N, K = d.shape
+    assert _lib().fh_op_mlp_pack(kind, ptr(d), ptr(out), N, K, None) == 0
+    return out
+
+
+@pytest.mark.parametrize("kind,N,K", [(1, 1536, 384), (1, 48, 64), (2, 384, 1536), (2, 384, 128)])
+def test_mlp_pack_is_the_documented_layout(kind, N, K):
+    rng = np.random.default_rng(N + K)
+    w = rng.standard_normal((N, K)).astype(np.float16)
+    got = mlp_pack(kind, dev(w)).cpu().numpy().reshape(-1, 8)
+    rows, cols = mlp_units(kind, N, K)
+    # every source element appears exactly once
+    assert len(set(zip(rows.tolist(), cols.tolist()))) == N * K // 8
+    np.testing.assert_array_equal(got, w[rows[:, None], cols[:, None] + np.arange(8)])
+
+
+# M covers each token-tile height the launcher picks on a 256-CU part (16·MT
+# rows per block, MT = 1..5) and partial last blocks; I covers 3 to 12 chunks.
+@pytest.mark.parametrize("M,I,bias", [(1, 1536, True), (13, 384, False), (1000, 1536, True), (4097, 1152, True),
+                                      (9000, 1536, False), (13000, 1536, True), (18048, 1536, True),
+                                      (20500, 1536, True)])
+def test_mlp_equals_the_two_folded_gemms(M, I, bias):
+    """The fused feed-forward block (fh_op_mlp) gives the same bits as its two
+    GEMMs run separately (LN_IN + GELU into a binary16 [M, I] buffer, then
+    RES_LN), and matches a float64 restatement of the block within float
+    tolerance: GELU(LN(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN(y) (native/model.go:607-633)
+    with LN(y) from the given row statistics."""
+    H = 384
+    rng = np.random.default_rng(M + I)
+    y = (rng.standard_normal((M, H)) * 3 + 1.5).astype(np.float16)
+    w1 = (rng.standard_normal((I, H)) * 0.05).astype(np.float16)
+    w2 = (rng.standard_normal((H, I)) * 0.05).astype(np.float16)
+    c1 = w1.astype(np.float64).sum(1).astype(np.float32)
+    c2 = rng.standard_normal(I).astype(np.float32)
+    b2 = rng.standard_normal(H).astype(np.float32) if bias else None
+    lg = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    lb = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    dy, dw1, dw2, dc1, dc2, dlg, dlb = dev(y), dev(w1), dev(w2), dev(c1), dev(c2), dev(lg), dev(lb)
+    db2 = dev(b2) if bias else None
+    w1p, w2r = torch.empty_like(dw1), torch.empty_like(dw2)
+    assert _lib().fh_op_ring_pack(ptr(dw1), ptr(w1p), I, H, None) == 0
+    assert _lib().fh_op_ring_pack(ptr(dw2), ptr(w2r), H, I, None) == 0
+    w1m, w2m = mlp_pack(1, dw1), mlp_pack(2, dw2)
+    st = row_stats(dy, 1e-12)
+    print(f"mlp M={M} I={I} bias={bias}", flush=True)
+    out = torch.empty((M, H), dtype=torch.float16, device="cuda")
+    assert _lib().fh_op_mlp(ptr(dy), ptr(st), ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
+                            ptr(out), M, H, I, None) == 0
+    sync()
+    got = out.cpu().numpy()
+    # the same block as two GEMMs, on the ring kernel and on the tiled one
+    for ring, b1, b2m in ((1, w1p, w2r), (0, dw1, dw2)):
+        h = torch.empty((M, I), dtype=torch.float16, device="cuda")
+        gemm_ln(ring, 1, dy, b1, h, st, 1, dc1, dc2)
+        ref = torch.empty((M, H), dtype=torch.float16, device="cuda")
+        want = gemm_ln(ring, 2, h, b2m, ref, st, bias=db2, yr=dy, lg=dlg, lb=dlb)
+        assert np.array_equal(got, want), (ring, int((got != want).sum()),
+                                           np.abs(got.astype(np.float64) - want).max())
+    if M <= 1000:
+        mean, rstd = st.cpu().numpy().astype(np.float64).T
+        y64 = y.astype(np.float64)
+        hh = gelu64(rstd[:, None] * (y64 @ w1.astype(np.float64).T - mean[:, None] * c1) + c2)
+        ref = (hh @ w2.astype(np.float64).T + (b2 if bias else 0.0) +
+               (y64 - mean[:, None]) * rstd[:, None] * lg + lb)
+        # h is rounded to binary16 before the second product
+        np.testing.assert_allclose(got.astype(np.float64), ref, atol=2e-3 * math.sqrt(I) / 4 + 4e-3, rtol=2e-3)
+
+
+def test_mlp_rejects_unfit_shapes():
+    from futon_amd import _lib as lib
+    d = dev(np.zeros((4096,), np.float16))
+    f = dev(np.zeros((4096,), np.float32))
+    args = (ptr(d), ptr(f), ptr(d), ptr(f), ptr(f), ptr(d), None, ptr(f), ptr(f), ptr(d))
+    assert _lib().fh_op_mlp(*args, 4, 256, 512, None) == lib.FH_EINVAL   # hidden width other than 384
+    assert _lib().fh_op_mlp(*args, 4, 384, 200, None) == lib.FH_EINVAL   # I % 128 != 0
+    assert _lib().fh_op_mlp(*args, 0, 384, 512, None) == 0               # nothing to do
+    assert _lib().fh_op_mlp(None, *args[1:], 4, 384, 512, None) == lib.FH_EINVAL
+
+
 @pytest.mark.parametrize("M,I,K", [(5, 32, 32), (70, 256, 64), (200, 1536, 384)])
 def test_gemm_swiglu_interleave(M, I, K):
     rng = np.random.default_rng(I + K)
