@@ -568,12 +568,14 @@ bool use_mlp(const DevLayer &L, int M, int I) {
 }
 
 // Fused FFN1 → GELU → FC2 with both LayerNorm folds (fh::mlp):
-// out = GELU(LN1(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN1(y), LN1 from y's statistics.
-int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, const f32x2 *stats, int M, f16 *out, hipStream_t s) {
+// out = GELU(LN1(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN1(y), LN1 from y's statistics
+// (computed in the kernel); stats_out, when set, receives out's statistics
+// for the next LayerNorm fold.
+int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, int M, f16 *out, f32x2 *stats_out, hipStream_t s) {
     const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
     MlpArgs g{};
     g.y = y;
-    g.stats = stats;
+    g.stats = nullptr;
     g.w1 = (const f16 *)L.ffn1.wm;
     g.c1 = L.ffn1_c1;
     g.c2 = L.ffn1_c2;
@@ -582,10 +584,12 @@ int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, const f32x2 *stats, 
     g.ln_g = L.n1w;
     g.ln_b = L.n1b;
     g.out = out;
+    g.stats_out = stats_out;
+    g.eps = (float)m->cfg.layer_norm_eps;
     g.M = M;
     g.I = I;
     const double flops = 4.0 * M * (double)H * I;
-    const double bytes = (double)M * H * 2 * 2 + 2.0 * H * I * 2 + M * 8.0;
+    const double bytes = (double)M * H * 2 * 2 + 2.0 * H * I * 2 + (stats_out ? M * 8.0 : 0.0);
     Scope sc(m, K_MLP, flops, bytes, s);
     LCHK(fh::mlp(g, s));
     return FH_OK;
@@ -655,6 +659,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, nullptr, nullptr, 0.f, H,
                           nullptr, m->x16, s));
     }
+    bool sa_ready = false;  // sA already holds yA's statistics (written by the previous fused block)
     for (int li = 0; li < c.num_layers; li++) {
         const DevLayer &L = m->layers[(size_t)li];
         if ((rc = checkpoint(m, b, cp, s))) return rc;
@@ -663,7 +668,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const float *bA = li ? m->layers[(size_t)li - 1].n2b : m->emb_b;
 
         // qkv = LN(yA)·Wqkvᵀ + b  (model.go:555)
-        if ((rc = row_stats(m, K_STATS, m->x16, T, m->sA, s)) ||
+        if ((!sa_ready && (rc = row_stats(m, K_STATS, m->x16, T, m->sA, s))) ||
             (rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
                             s)))
             return rc;
@@ -704,8 +709,12 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // h = act(LN1(yB)·W1ᵀ + b1); yA = h·W2ᵀ + b2 + LN1(yB)  (model.go:607-633)
+        sa_ready = false;
         if (use_mlp(L, M, I)) {
-            if ((rc = row_stats(m, K_STATS, yBo, M, sB, s)) || (rc = mlp_fused(m, L, yBo, sB, M, yA, s))) return rc;
+            // The block computes yB's statistics itself and, unless this is
+            // the last layer, yA's for the next layer's QKV fold.
+            if ((rc = mlp_fused(m, L, yBo, M, yA, last ? nullptr : m->sA, s))) return rc;
+            sa_ready = !last;
             continue;
         }
         if ((rc = row_stats(m, last_cls ? K_CLS_TAIL : K_STATS, yBo, M, sB, s)) ||

@@ -50,13 +50,15 @@ struct GemmArgs {
 // out = GELU(rstd·(y·W1ᵀ − mean·c1) + c2)·W2ᵀ + b2 + ((y − mean)·rstd·γ + β).
 struct MlpArgs {
     const f16 *y;              // [M, 384] un-normalized LayerNorm input
-    const f32x2 *stats;        // [M] (mean, rstd) of y's rows
+    const f32x2 *stats;        // [M] (mean, rstd) of y's rows, or null: computed from y (row_stats' order)
     const f16 *w1;             // fc1 weights [I, 384] scaled by γ, fragment-ordered (mlp_w1_unit)
     const float *c1, *c2;      // [I] LayerNorm fold terms of fc1 (c2 includes fc1's bias)
     const f16 *w2;             // fc2 weights [384, I], fragment-ordered (mlp_w2_unit)
     const float *b2;           // [384] fc2 bias, or null
     const float *ln_g, *ln_b;  // [384] γ, β of y's LayerNorm (the residual)
     f16 *out;                  // [M, 384]
+    f32x2 *stats_out;          // [M] (mean, rstd) of out's rows, or null
+    float eps;                 // LayerNorm epsilon of both statistics
     int M, I;
 };
 

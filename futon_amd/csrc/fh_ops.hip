@@ -126,8 +126,8 @@ extern "C" int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N,
 
 extern "C" int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const float *c1, const float *c2,
                          const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
-                         int32_t M, int32_t H, int32_t I, void *stream) {
-    if (!y || !stats || !w1_packed || !c1 || !c2 || !w2_packed || !ln_g || !ln_b || !out || M < 0) return FH_EINVAL;
+                         void *stats_out, float eps, int32_t M, int32_t H, int32_t I, void *stream) {
+    if (!y || !w1_packed || !c1 || !c2 || !w2_packed || !ln_g || !ln_b || !out || M < 0) return FH_EINVAL;
     if (M == 0) return FH_OK;
     if (!fh::mlp_ok(M, H, I)) return FH_EINVAL;
     MlpArgs g{};
@@ -141,6 +141,8 @@ extern "C" int fh_op_mlp(const void *y, const void *stats, const void *w1_packed
     g.ln_g = ln_g;
     g.ln_b = ln_b;
     g.out = (f16 *)out;
+    g.stats_out = (f32x2 *)stats_out;
+    g.eps = eps;
     g.M = M;
     g.I = I;
     return code_of(fh::mlp(g, (hipStream_t)stream));

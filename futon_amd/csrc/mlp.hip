@@ -34,6 +34,7 @@
 #include "fh_common.h"
 #include "gemm_epi.h"
 #include "lds_dma.h"
+#include "row_stats.h"
 
 namespace {
 using namespace fh_epi;
@@ -62,7 +63,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
     constexpr int H_BYTES = (CH / 64) * BM * ROWB;  // one chunk's h, k-block major
     constexpr int C_OFF = A_BYTES + 2 * H_BYTES;    // c1 [I_MAX] then c2 [I_MAX] (f32)
-    constexpr int S_OFF = C_OFF + 2 * I_MAX * 4;    // (mean, rstd) of the tile's rows
+    // After the chunk loop the h/c region holds the output tile (same layout
+    // as the token tile) for the row statistics and coalesced stores.
+    constexpr int O_OFF = A_BYTES, S_OFF = A_BYTES + (2 * H_BYTES + 2 * I_MAX * 4 > A_BYTES ? 2 * H_BYTES + 2 * I_MAX * 4 : A_BYTES);
     constexpr int TS = MT;                          // epilogue tiles done beside phase 2 (all)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S_OFF + BM * 8];
     const uint8_t *const atile = lds;
@@ -96,8 +99,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
 #pragma unroll
         for (int t = 0; t < NT2; ++t) w2f[ks][t] = w2p[(ks * NT2 + t) * 64];
 
-    // Row statistics of the tile's rows (rows past M clamped: never stored).
-    if ((int)threadIdx.x < BM) lst[threadIdx.x] = g.stats[min(m0 + (int)threadIdx.x, g.M - 1)];
+    // Row statistics of the tile's rows, when given (rows past M clamped:
+    // never stored).
+    if (g.stats && (int)threadIdx.x < BM) lst[threadIdx.x] = g.stats[min(m0 + (int)threadIdx.x, g.M - 1)];
 
     // Into LDS: the token tile (DMA block b = rows 8·(b % 2MT) .. of k-block
     // b / 2MT; a block is 8 rows, lane l writing physical chunk l%8 of row l/8,
@@ -126,6 +130,31 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     // Everything above has landed (the weights were requested first, so
     // their latency overlaps the tile's) and every wave's part is visible.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // (mean, rstd) of a tile's rows in row_stats' order: 16 lanes per row,
+    // lane l16 holding 16-byte chunks c·16 + l16; each row's result goes to
+    // dst(r, stats) from lane 0 of each row.  The conditions are uniform per
+    // wave (BM % 4 == 0).
+    auto tile_stats = [&](const uint8_t *tile, auto dst) {
+        const int l16 = lane & 15;
+#pragma unroll
+        for (int r0 = 0; r0 < BM; r0 += NW * 4) {
+            const int r = r0 + wave * 4 + (lane >> 4);
+            if (r0 + wave * 4 < BM) {
+                f16x8 v[HD / 128];
+#pragma unroll
+                for (int c = 0; c < HD / 128; ++c) {
+                    const int q = c * 16 + l16;
+                    v[c] = *(const f16x8 *)(tile + (q >> 3) * BM * ROWB + r * ROWB + (((q & 7) ^ (r & 7)) << 4));
+                }
+                const f32x2 st = fh_rs::row_stats16<HD / 128>(v, g.eps);
+                if (l16 == 0) dst(r, st);
+            }
+        }
+    };
+    if (!g.stats) {
+        tile_stats(atile, [&](int r, f32x2 st) { lst[r] = st; });
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
 
     // Fragment offsets inside a 16-row group: row lane%16, logical chunk
     // lane/16 + 4·(ks%2) at physical chunk ^ (lane%8).
@@ -235,8 +264,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
 
     // Output epilogue: acc + b2 + (y − mean)·rstd·γ + β, rounded once; y read
     // back from the resident token tile.  This lane's outputs:
-    // n0 = 16·NT2·wave + 4·NT2·(lane/16) + {0 .. 4·NT2 − 1}.
-    const __amdgpu_buffer_rsrc_t rO = buf_rsrc(g.out, (uint32_t)g.M * (HD * 2));
+    // n0 = 16·NT2·wave + 4·NT2·(lane/16) + {0 .. 4·NT2 − 1}.  The binary16
+    // results go to the output tile in LDS (the h/c region, free once every
+    // wave has left the chunk loop), whose rows are then stored with 16-byte
+    // coalesced stores and, when asked, reduced to their statistics.
     const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
     f32x4 kb[NT2], kg[NT2], kt[NT2];
 #pragma unroll
@@ -245,24 +276,40 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         kg[t] = *(const f32x4 *)(g.ln_g + n0 + 4 * t);
         kt[t] = *(const f32x4 *)(g.ln_b + n0 + 4 * t);
     }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    uint8_t *const otile = lds + O_OFF;
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm) {
         const int r = tm * 16 + (lane & 15);
+        const f32x2 sv = lst[r];
 #pragma unroll
         for (int t = 0; t < NT2; ++t) {
             const int n = n0 + 4 * t;
-            const f16x4 y4 = *(const f16x4 *)(atile + (n >> 6) * BM * ROWB + r * ROWB +
-                                              ((((n & 63) >> 3) ^ (lane & 7)) << 4) + (n & 7) * 2);
+            const int off = (n >> 6) * BM * ROWB + r * ROWB + ((((n & 63) >> 3) ^ (lane & 7)) << 4) + (n & 7) * 2;
+            const f16x4 y4 = *(const f16x4 *)(atile + off);
             f32x4 x = acc2[t][tm];
             if (BIAS) x += kb[t];
-            x += ln_resid_v(y4, lst[r], kg[t], kt[t]);
+            x += ln_resid_v(y4, sv, kg[t], kt[t]);
             f16x4 o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rO, (uint32_t)((m0 + r) * HD + n) * 2,
-                                                  0, 0);
+            *(f16x4 *)(otile + off) = o;
         }
     }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    {
+        const __amdgpu_buffer_rsrc_t rO = buf_rsrc(g.out, (uint32_t)g.M * (HD * 2));
+        constexpr int UPR = HD * 2 / 16;  // 16-byte units per row
+        for (int u = (int)threadIdx.x; u < BM * UPR; u += 64 * NW) {
+            const int r = u / UPR, cu = u - r * UPR;
+            const i32x4 v = *(const i32x4 *)(otile + (cu >> 3) * BM * ROWB + r * ROWB + (((cu & 7) ^ (r & 7)) << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(v, rO, (uint32_t)((m0 + r) * HD * 2 + cu * 16), 0, 0);
+        }
+    }
+    if (g.stats_out)
+        tile_stats(otile, [&](int r, f32x2 st) {
+            if (m0 + r < g.M) g.stats_out[m0 + r] = st;
+        });
 }
 
 // out = the fragment-ordered copy of B, 16 bytes per thread.
@@ -313,7 +360,7 @@ bool mlp_ok(int M, int H, int I) {
 }
 
 hipError_t mlp(const MlpArgs &g, hipStream_t s) {
-    if (!mlp_ok(g.M, HD, g.I) || !g.y || !g.stats || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
+    if (!mlp_ok(g.M, HD, g.I) || !g.y || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
         return hipErrorInvalidValue;
     const int ncu = cu_count();
     if (ncu <= 0) return hipErrorUnknown;

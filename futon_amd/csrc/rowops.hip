@@ -6,6 +6,7 @@
 // variance accumulated in float64, inv = float32(1/sqrt(var + eps)),
 // y = (x - float32(mean))·inv·γ + β.  One wavefront per row.
 #include "fh_common.h"
+#include "row_stats.h"
 
 namespace {
 
@@ -226,21 +227,6 @@ __device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL]
     st_row<VPL>(o32, o16, lane, v);
 }
 
-// Sum over each 16-lane DPP row (xor 1, xor 2, half-row mirror, row mirror:
-// the row total lands in all 16 lanes), in float64 as two 32-bit halves.
-template <int CTRL>
-__device__ __forceinline__ double dpp_step_f64(double v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)__double2loint(v), CTRL, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)__double2hiint(v), CTRL, 0xF, 0xF, false);
-    return v + __hiloint2double(hi, lo);
-}
-__device__ __forceinline__ double row16_sum_f64(double v) {
-    v = dpp_step_f64<0xB1>(v);
-    v = dpp_step_f64<0x4E>(v);
-    v = dpp_step_f64<0x141>(v);
-    return dpp_step_f64<0x140>(v);
-}
-
 // (mean, rstd) per row of binary16 y [M, 128·C]: 16 lanes per row, C
 // 16-byte chunks per lane, four rows per wave.  Σy and Σy² in float64
 // (Σy exact for binary16 data), mean = Σy/H, var = Σy²/H − mean² in float64,
@@ -256,20 +242,8 @@ __global__ __launch_bounds__(256) void row_stats_kernel(const f16 *y, int M, flo
     f16x8 v[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) v[c] = *(const f16x8 *)(y + (size_t)r * H + (c * 16 + l16) * 8);
-    double s1 = 0.0, s2 = 0.0;
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const double x = (double)(float)v[c][e];
-            s1 += x;
-            s2 = fma(x, x, s2);
-        }
-    s1 = row16_sum_f64(s1);
-    s2 = row16_sum_f64(s2);
-    const double mean = s1 / H;
-    const double var = fmax(s2 / H - mean * mean, 0.0);
-    if (l16 == 0 && row < M) st[row] = (f32x2){(float)mean, (float)(1.0 / sqrt(var + (double)eps))};
+    const f32x2 s = fh_rs::row_stats16<C>(v, eps);
+    if (l16 == 0 && row < M) st[row] = s;
 }
 
 // Two rows per wave: both rows and γ/β are requested before any reduction,

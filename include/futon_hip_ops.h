@@ -80,17 +80,20 @@ int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream
 int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N, int32_t K, void *stream);
 
 /* The encoder layer's feed-forward block in one kernel, hidden width H = 384,
- * GELU, I % 128 == 0:
+ * GELU, I % 128 == 0, I <= 2048:
  *   out = GELU(rstd·(y·W1ᵀ − mean·c1) + c2)·W2ᵀ + b2 + (y − mean)·rstd·ln_g + ln_b
- * y [M, 384] binary16 (un-normalized), stats [M] (mean, rstd) float pairs of
- * y's rows (fh_op_row_stats), w1_packed = fh_op_mlp_pack kind 1 of W1 [I, 384],
- * w2_packed = kind 2 of W2 [384, I], b2 may be NULL; out [M, 384]
- * binary16.  The intermediate GELU output never reaches memory; the result
- * has the same bits as fh_op_gemm_ln LN_IN + GELU followed by RES_LN.
- * Replaces: the MLP block of the encoder layer (native/model.go:607-633). */
+ * y [M, 384] binary16 (un-normalized); stats [M] (mean, rstd) float pairs of
+ * y's rows, or NULL to compute them in the kernel (the same bits as
+ * fh_op_row_stats with eps); w1_packed = fh_op_mlp_pack kind 1 of W1
+ * [I, 384], w2_packed = kind 2 of W2 [384, I], b2 may be NULL; out [M, 384]
+ * binary16; stats_out, when not NULL, receives fh_op_row_stats(out, eps).
+ * The intermediate GELU output never reaches memory; the result has the same
+ * bits as fh_op_gemm_ln LN_IN + GELU followed by RES_LN.
+ * Replaces: the MLP block of the encoder layer (native/model.go:607-633) and
+ * the statistics of the LayerNorms on either side (:741-770). */
 int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const float *c1, const float *c2,
-              const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out, int32_t M,
-              int32_t H, int32_t I, void *stream);
+              const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
+              void *stats_out, float eps, int32_t M, int32_t H, int32_t I, void *stream);
 
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,

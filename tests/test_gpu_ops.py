@@ -308,13 +308,22 @@ def test_mlp_equals_the_two_folded_gemms(M, I, bias):
     assert _lib().fh_op_ring_pack(ptr(dw1), ptr(w1p), I, H, None) == 0
     assert _lib().fh_op_ring_pack(ptr(dw2), ptr(w2r), H, I, None) == 0
     w1m, w2m = mlp_pack(1, dw1), mlp_pack(2, dw2)
-    st = row_stats(dy, 1e-12)
+    eps = 1e-12
+    st = row_stats(dy, eps)
     print(f"mlp M={M} I={I} bias={bias}", flush=True)
-    out = torch.empty((M, H), dtype=torch.float16, device="cuda")
-    assert _lib().fh_op_mlp(ptr(dy), ptr(st), ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
-                            ptr(out), M, H, I, None) == 0
-    sync()
-    got = out.cpu().numpy()
+    outs = []
+    for given in (True, False):
+        out = torch.empty((M, H), dtype=torch.float16, device="cuda")
+        so = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+        assert _lib().fh_op_mlp(ptr(dy), ptr(st) if given else None, ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m),
+                                ptr(db2), ptr(dlg), ptr(dlb), ptr(out), ptr(so), eps, M, H, I, None) == 0
+        sync()
+        # the block's output statistics are row_stats of its output, bit for bit
+        assert np.array_equal(so.cpu().numpy(), row_stats(out, eps).cpu().numpy())
+        outs.append(out.cpu().numpy())
+    # statistics computed in the kernel are row_stats' bits: same output
+    assert np.array_equal(outs[0], outs[1])
+    got = outs[0]
     # the same block as two GEMMs, on the ring kernel and on the tiled one
     for ring, b1, b2m in ((1, w1p, w2r), (0, dw1, dw2)):
         h = torch.empty((M, I), dtype=torch.float16, device="cuda")
@@ -337,9 +346,10 @@ def test_mlp_rejects_unfit_shapes():
     from futon_amd import _lib as lib
     d = dev(np.zeros((4096,), np.float16))
     f = dev(np.zeros((4096,), np.float32))
-    args = (ptr(d), ptr(f), ptr(d), ptr(f), ptr(f), ptr(d), None, ptr(f), ptr(f), ptr(d))
+    args = (ptr(d), ptr(f), ptr(d), ptr(f), ptr(f), ptr(d), None, ptr(f), ptr(f), ptr(d), None, 1e-12)
     assert _lib().fh_op_mlp(*args, 4, 256, 512, None) == lib.FH_EINVAL   # hidden width other than 384
     assert _lib().fh_op_mlp(*args, 4, 384, 200, None) == lib.FH_EINVAL   # I % 128 != 0
+    assert _lib().fh_op_mlp(*args, 4, 384, 2176, None) == lib.FH_EINVAL  # I above 2048
     assert _lib().fh_op_mlp(*args, 0, 384, 512, None) == 0               # nothing to do
     assert _lib().fh_op_mlp(None, *args[1:], 4, 384, 512, None) == lib.FH_EINVAL
 
