@@ -17,6 +17,8 @@
 // from registers (the key order inside the contraction is permuted
 // identically on both operands).  Q fragments are loaded from global memory
 // directly in the MFMA operand layout.
+#include <type_traits>
+
 #include "fh_common.h"
 
 namespace {
@@ -137,22 +139,25 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
         const int kvalid = L - kb0;                   // valid keys from kb0 on
         const int nkt = min(NKT, (kvalid + 15) >> 4);  // key tiles holding valid keys
 
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            if (q0 + (wave * QT + qt) * 16 >= nq) continue;  // tile holds no live query (wave-uniform)
+        // One query tile against this key block's NV valid key tiles (NV is
+        // uniform across the block, so each count gets its own straight-line
+        // code: scores, exponentials and PV chunks only for valid keys, the
+        // mask only on the last tile).
+        auto qtile = [&](auto nv_c, int qt) {
+            constexpr int NV = decltype(nv_c)::value;
+            constexpr int NC = (NV + 1) / 2;  // 32-key PV chunks
             // Sᵀ tiles: s[kt][i] = score(key kb0 + kt·16 + (lane/16)·4 + i, query lane%16).
-            f32x4 s[NKT];
+            f32x4 s[NV];
             float mx = -INFINITY;
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) {
-                if (kt >= nkt) continue;
+            for (int kt = 0; kt < NV; ++kt) {
                 s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int dk = 0; dk < D / 32; ++dk) {
                     const f16x8 kf = *(const f16x8 *)&Ks[(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
                     s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qt][dk], s[kt], 0, 0, 0);
                 }
-                if (kt * 16 + 16 > kvalid) {  // boundary tile: mask keys past the sequence
+                if (kt == NV - 1 && kt * 16 + 16 > kvalid) {  // boundary tile: mask keys past the sequence
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         if (kt * 16 + (lane >> 4) * 4 + i >= kvalid) s[kt][i] = -INFINITY;
@@ -164,12 +169,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
             const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
             const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
             float psum = 0.f;
-            f16x8 pf[NKT / 2];
+            f16x8 pf[NC];
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt)
+            for (int kt = 0; kt < 2 * NC; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float p = kt < nkt ? __builtin_amdgcn_exp2f(s[kt][i] * sl2 - m_new) : 0.f;
+                    const float p = kt < NV ? __builtin_amdgcn_exp2f(s[kt < NV ? kt : 0][i] * sl2 - m_new) : 0.f;
                     psum += p;
                     pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
                 }
@@ -182,8 +187,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
 
             // Oᵀ += Vᵀ·Pᵀ over 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
 #pragma unroll
-            for (int c = 0; c < NKT / 2; ++c) {
-                if (2 * c >= nkt) continue;
+            for (int c = 0; c < NC; ++c) {
 #pragma unroll
                 for (int t = 0; t < D / 16; ++t) {
                     const f16 *vrow = &Vt[(t * 16 + (lane & 15)) * VS + c * 32 + (lane >> 4) * 4];
@@ -192,6 +196,21 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
                     const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[qt][t], 0, 0, 0);
                 }
+            }
+        };
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            if (q0 + (wave * QT + qt) * 16 >= nq) continue;  // tile holds no live query (wave-uniform)
+            static_assert(NKT <= 8, "key tiles per block");
+            switch (nkt) {
+            case 1: qtile(std::integral_constant<int, 1>{}, qt); break;
+            case 2: qtile(std::integral_constant<int, 2>{}, qt); break;
+            case 3: if constexpr (NKT >= 3) qtile(std::integral_constant<int, (NKT >= 3 ? 3 : 1)>{}, qt); break;
+            case 4: if constexpr (NKT >= 4) qtile(std::integral_constant<int, (NKT >= 4 ? 4 : 1)>{}, qt); break;
+            case 5: if constexpr (NKT >= 5) qtile(std::integral_constant<int, (NKT >= 5 ? 5 : 1)>{}, qt); break;
+            case 6: if constexpr (NKT >= 6) qtile(std::integral_constant<int, (NKT >= 6 ? 6 : 1)>{}, qt); break;
+            case 7: if constexpr (NKT >= 7) qtile(std::integral_constant<int, (NKT >= 7 ? 7 : 1)>{}, qt); break;
+            default: qtile(std::integral_constant<int, NKT>{}, qt); break;
             }
         }
     }
