@@ -561,21 +561,33 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     return FH_OK;
 }
 
-// Whether layer L's feed-forward block runs fused for M rows: its fc2 copy
-// for fh::mlp exists and M is large enough for the ring-sized path.
+// Whether layer L's output projection and feed-forward block run fused for
+// M rows: the fragment-ordered copies exist and M is large enough for the
+// ring-sized path.
 bool use_mlp(const DevLayer &L, int M, int I) {
-    return L.fc2.wm && L.ffn1.wm && fh::gemm_ring_worth(M, I) && fh::mlp_ok(M, L.fc2.n, I);
+    return L.fc2.wm && L.ffn1.wm && L.out.wm && fh::gemm_ring_worth(M, I) && fh::mlp_ok(M, L.fc2.n, I);
 }
 
-// Fused FFN1 → GELU → FC2 with both LayerNorm folds (fh::mlp):
-// out = GELU(LN1(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN1(y), LN1 from y's statistics
-// (computed in the kernel); stats_out, when set, receives out's statistics
-// for the next LayerNorm fold.
-int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, int M, f16 *out, f32x2 *stats_out, hipStream_t s) {
+// The rest of the layer after attention in one kernel (fh::mlp with the
+// output projection): y = attn·Woᵀ + bo + LNa(ya) (ya's statistics in
+// stats_a, γa/βa the previous norm2 or the embedding LayerNorm), then
+// out = GELU(LN1(y)·W1ᵀ + b1)·W2ᵀ + b2 + LN1(y), LN1's statistics computed in
+// the kernel; stats_out, when set, receives out's statistics for the next
+// LayerNorm fold.  out may alias ya and stats_out stats_a (rows belong to
+// one block, which reads them before it writes).
+int mlp_fused(fh_model *m, const DevLayer &L, const f16 *attn, const f16 *ya, const f32x2 *stats_a,
+              const float *ga, const float *ba, int M, f16 *out, f32x2 *stats_out, hipStream_t s) {
     const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
     MlpArgs g{};
-    g.y = y;
+    g.y = nullptr;
     g.stats = nullptr;
+    g.attn = attn;
+    g.wo = (const f16 *)L.out.wm;
+    g.bo = L.out_b;
+    g.ya = ya;
+    g.stats_a = stats_a;
+    g.ga = ga;
+    g.ba = ba;
     g.w1 = (const f16 *)L.ffn1.wm;
     g.c1 = L.ffn1_c1;
     g.c2 = L.ffn1_c2;
@@ -588,8 +600,8 @@ int mlp_fused(fh_model *m, const DevLayer &L, const f16 *y, int M, f16 *out, f32
     g.eps = (float)m->cfg.layer_norm_eps;
     g.M = M;
     g.I = I;
-    const double flops = 4.0 * M * (double)H * I;
-    const double bytes = (double)M * H * 2 * 2 + 2.0 * H * I * 2 + (stats_out ? M * 8.0 : 0.0);
+    const double flops = 4.0 * M * (double)H * I + 2.0 * M * (double)H * H;
+    const double bytes = (double)M * H * 2 * 3 + 2.0 * H * I * 2 + 2.0 * H * H + M * 8.0 + (stats_out ? M * 8.0 : 0.0);
     Scope sc(m, K_MLP, flops, bytes, s);
     LCHK(fh::mlp(g, s));
     return FH_OK;
@@ -703,20 +715,25 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1;
         const int kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
 
+        sa_ready = false;
+        if (use_mlp(L, M, I)) {
+            // yB = attn·Woᵀ + b + LN(yA), then the feed-forward block, in one
+            // kernel: yB stays on-chip, its statistics are computed there,
+            // and (unless this is the last layer) so are the new yA's for the
+            // next layer's QKV fold.  The checkpoint between the two
+            // (model.go:603) is taken before the launch.
+            if ((rc = checkpoint(m, b, cp, s)) ||
+                (rc = mlp_fused(m, L, (const f16 *)m->attn, yA, sA, gA, bA, M, yA, last ? nullptr : m->sA, s)))
+                return rc;
+            sa_ready = !last;
+            continue;
+        }
         // yB = attn·Woᵀ + b + LN(yA)  (model.go:596-599)
         if ((rc = gemm_resln(m, kOut, L.out, last_cls ? m->attnc : m->attn, M, L.out_b, yA, sA, gA, bA, yBo, s)))
             return rc;
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // h = act(LN1(yB)·W1ᵀ + b1); yA = h·W2ᵀ + b2 + LN1(yB)  (model.go:607-633)
-        sa_ready = false;
-        if (use_mlp(L, M, I)) {
-            // The block computes yB's statistics itself and, unless this is
-            // the last layer, yA's for the next layer's QKV fold.
-            if ((rc = mlp_fused(m, L, yBo, M, yA, last ? nullptr : m->sA, s))) return rc;
-            sa_ready = !last;
-            continue;
-        }
         if ((rc = row_stats(m, last_cls ? K_CLS_TAIL : K_STATS, yBo, M, sB, s)) ||
             (rc = gemm_lnin(m, kFfn1, L.ffn1, yBo, M, L.ffn1_c1, L.ffn1_c2, sB, m->hbuf, I,
                             swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU, s)))
@@ -966,7 +983,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
         if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8, ring_fits(3 * H, H)))) return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.qkv.bias"), 3 * H, &L.qkv_b, true))) return bail(rc);
         if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) ||
-            (rc = upload_mat(m, L.out, w, H, H, q8, ring_fits(H, H))))
+            (rc = upload_mat(m, L.out, w, H, H, q8, ring_fits(H, H), mlp_on ? 2 : 0)))
             return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.out.bias"), H, &L.out_b, true))) return bail(rc);
         if ((rc = ld.vec_f32(nm("norm1.weight"), H, &L.n1w)) || (rc = ld.vec_f32(nm("norm1.bias"), H, &L.n1b)))

@@ -58,6 +58,15 @@ struct MlpArgs {
     const float *ln_g, *ln_b;  // [384] γ, β of y's LayerNorm (the residual)
     f16 *out;                  // [M, 384]
     f32x2 *stats_out;          // [M] (mean, rstd) of out's rows, or null
+    // Optional output projection ahead of the block (attn non-null): y is
+    // then yB = attn·Woᵀ + bo + ((ya − mean)·rstd·γa + βa), built on-chip
+    // (y itself is unused and stats must be null).
+    const f16 *attn;           // [M, 384] attention output, or null
+    const f16 *wo;             // Wo [384, 384], fragment-ordered (mlp_w2_unit)
+    const float *bo;           // [384] or null
+    const f16 *ya;             // [M, 384] un-normalized input of the attention block's LayerNorm
+    const f32x2 *stats_a;      // [M] (mean, rstd) of ya's rows
+    const float *ga, *ba;      // [384] γ, β of that LayerNorm
     float eps;                 // LayerNorm epsilon of both statistics
     int M, I;
 };

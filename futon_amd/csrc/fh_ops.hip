@@ -148,6 +148,39 @@ extern "C" int fh_op_mlp(const void *y, const void *stats, const void *w1_packed
     return code_of(fh::mlp(g, (hipStream_t)stream));
 }
 
+extern "C" int fh_op_outproj_mlp(const void *attn, const void *wo_packed, const float *bo, const void *ya,
+                                 const void *stats_a, const float *ga, const float *ba, const void *w1_packed,
+                                 const float *c1, const float *c2, const void *w2_packed, const float *b2,
+                                 const float *ln_g, const float *ln_b, void *out, void *stats_out, float eps,
+                                 int32_t M, int32_t H, int32_t I, void *stream) {
+    if (!attn || !wo_packed || !ya || !stats_a || !ga || !ba || !w1_packed || !c1 || !c2 || !w2_packed || !ln_g ||
+        !ln_b || !out || M < 0)
+        return FH_EINVAL;
+    if (M == 0) return FH_OK;
+    if (!fh::mlp_ok(M, H, I)) return FH_EINVAL;
+    MlpArgs g{};
+    g.attn = (const f16 *)attn;
+    g.wo = (const f16 *)wo_packed;
+    g.bo = bo;
+    g.ya = (const f16 *)ya;
+    g.stats_a = (const f32x2 *)stats_a;
+    g.ga = ga;
+    g.ba = ba;
+    g.w1 = (const f16 *)w1_packed;
+    g.c1 = c1;
+    g.c2 = c2;
+    g.w2 = (const f16 *)w2_packed;
+    g.b2 = b2;
+    g.ln_g = ln_g;
+    g.ln_b = ln_b;
+    g.out = (f16 *)out;
+    g.stats_out = (f32x2 *)stats_out;
+    g.eps = eps;
+    g.M = M;
+    g.I = I;
+    return code_of(fh::mlp(g, (hipStream_t)stream));
+}
+
 extern "C" int fh_op_attention(const void *qkv, const int32_t *offsets, int32_t nseq, int32_t max_len, int32_t H,
                                int32_t heads, const float *rope_cos, const float *rope_sin, void *out,
                                int32_t q_limit, int32_t compact, int32_t out_f32, void *stream) {

@@ -57,7 +57,7 @@ constexpr int W1C = NW * KS1 * NT1 * 64;  // 16-byte units of W1 per chunk
 constexpr int W2C = NW * KS2 * NT2 * 64;  // 16-byte units of W2 per chunk
 static_assert(CH == NW * 16 * NT1 && NT2 * 16 * NW == HD, "wave split");
 
-template <int MT, bool BIAS>
+template <int MT, bool BIAS, bool OUTP>
 __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     constexpr int BM = 16 * MT;
     constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
@@ -84,40 +84,44 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     const i32x4 *w1p = (const i32x4 *)g.w1 + (size_t)wave * KS1 * NT1 * 64 + lane;
     const i32x4 *w2p = (const i32x4 *)g.w2 + (size_t)wave * KS2 * NT2 * 64 + lane;
     i32x4 w1f[W1H][NT1], w2f[KS2][NT2];
+    auto prefetch_w = [&] {
 #pragma unroll
-    for (int ks = 0; ks < W1H; ++ks)
+        for (int ks = 0; ks < W1H; ++ks)
 #pragma unroll
-        for (int tn = 0; tn < NT1; ++tn) w1f[ks][tn] = w1p[(ks * NT1 + tn) * 64];
+            for (int tn = 0; tn < NT1; ++tn) w1f[ks][tn] = w1p[(ks * NT1 + tn) * 64];
+#pragma unroll
+        for (int ks = 0; ks < KS2; ++ks)
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) w2f[ks][t] = w2p[(ks * NT2 + t) * 64];
+    };
     // After multiplying k-step ks of chunk c: refill its slot.
     auto w1_refill = [&](int c, int ks) {
         const int cc = ks < W1H ? c : min(c + 1, nchunk - 1), kk = ks < W1H ? ks + W1H : ks - W1H;
 #pragma unroll
         for (int tn = 0; tn < NT1; ++tn) w1f[ks % W1H][tn] = w1p[(size_t)cc * W1C + (kk * NT1 + tn) * 64];
     };
-#pragma unroll
-    for (int ks = 0; ks < KS2; ++ks)
-#pragma unroll
-        for (int t = 0; t < NT2; ++t) w2f[ks][t] = w2p[(ks * NT2 + t) * 64];
-
     // Row statistics of the tile's rows, when given (rows past M clamped:
     // never stored).
-    if (g.stats && (int)threadIdx.x < BM) lst[threadIdx.x] = g.stats[min(m0 + (int)threadIdx.x, g.M - 1)];
+    if (!OUTP && g.stats && (int)threadIdx.x < BM) lst[threadIdx.x] = g.stats[min(m0 + (int)threadIdx.x, g.M - 1)];
 
-    // Into LDS: the token tile (DMA block b = rows 8·(b % 2MT) .. of k-block
-    // b / 2MT; a block is 8 rows, lane l writing physical chunk l%8 of row l/8,
-    // i.e. logical chunk (l%8) ^ (l/8)) and the fold terms c1, c2 (1 KB per
-    // block, lane-linear).  Blocks wave, wave + NW, ...
-    {
-        const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
-        const __amdgpu_buffer_rsrc_t rY = buf_rsrc(g.y, (uint32_t)g.M * (HD * 2));
+    // DMA of a [BM, 384] binary16 tile of rows m0.. into LDS at `dst`
+    // (k-block major, the swizzled layout): block b = rows 8·(b % 2MT) .. of
+    // k-block b / 2MT, lane l writing physical chunk l%8 of row l/8, i.e.
+    // logical chunk (l%8) ^ (l/8); blocks wave, wave + NW, ...  Rows past M
+    // read as zero.  Then the fold terms c1, c2 (1 KB per block, lane-linear).
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+    auto dma_tile = [&](const f16 *src, uint32_t dst) {
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, (uint32_t)g.M * (HD * 2));
         const uint32_t lrow = lane >> 3, lchunk = ((lane & 7) ^ (lane >> 3)) * 16;
 #pragma unroll
         for (int i = 0; i < (12 * MT + NW - 1) / NW; ++i) {
             const int b = wave + NW * i, kb = b / (2 * MT), rb = b - kb * 2 * MT;
             if (b < 12 * MT)
-                dma16(rY, lds0 + (uint32_t)b * 1024, (uint32_t)(m0 + rb * 8 + (int)lrow) * (HD * 2) + lchunk,
+                dma16(rs, dst + (uint32_t)b * 1024, (uint32_t)(m0 + rb * 8 + (int)lrow) * (HD * 2) + lchunk,
                       (uint32_t)kb * ROWB);
         }
+    };
+    auto dma_fold_terms = [&] {
         const __amdgpu_buffer_rsrc_t rC1 = buf_rsrc(g.c1, (uint32_t)g.I * 4);
         const __amdgpu_buffer_rsrc_t rC2 = buf_rsrc(g.c2, (uint32_t)g.I * 4);
         const int ncb = (g.I * 4 + 1023) / 1024;
@@ -126,10 +130,87 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
             dma16(which ? rC2 : rC1, lds0 + C_OFF + (uint32_t)which * (I_MAX * 4) + (uint32_t)kb * 1024,
                   (uint32_t)lane * 16, (uint32_t)kb * 1024);
         }
+    };
+    // Fragment offsets inside a 16-row group: row lane%16, logical chunk
+    // lane/16 + 4·(ks%2) at physical chunk ^ (lane%8).
+    int fo[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) fo[k] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * k) ^ (lane & 7)) << 4);
+
+    if constexpr (OUTP) {
+        // Phase 0, the attention output projection (the out-projection GEMM's
+        // RES_LN form, same K order and epilogue arithmetic): the attention
+        // tile goes to the h/c region, Wo fragments stream through registers
+        // four k-steps ahead, and yB = attn·Woᵀ + bo + LN_a(ya) is written in
+        // binary16 into the token tile.  This lane's outputs: the same
+        // n0 + {0..4·NT2−1} as the final epilogue.
+        dma_tile(g.attn, lds0 + O_OFF);
+        const i32x4 *w0p = (const i32x4 *)g.wo + (size_t)wave * KS2 * NT2 * 64 + lane;
+        i32x4 w0f[KS2][NT2];
+#pragma unroll
+        for (int ks = 0; ks < KS2; ++ks)
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) w0f[ks][t] = w0p[(ks * NT2 + t) * 64];
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        f32x4 acc0[NT2][MT];
+#pragma unroll
+        for (int k = 0; k < KS1; ++k) {
+            const uint8_t *ab = lds + O_OFF + (k >> 1) * BM * ROWB + fo[k & 1];
+            i32x4 af[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+#pragma unroll
+                for (int tm = 0; tm < MT; ++tm)
+                    acc0[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, w0f[k % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
+                        k == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc0[t][tm], 0, 0, 0);
+                if (k + KS2 < KS1) {
+                    const int kn = k + KS2;
+                    w0f[k % KS2][t] = w0p[(size_t)(kn / KS2) * W2C + ((kn % KS2) * NT2 + t) * 64];
+                }
+            }
+        }
+        const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
+        f32x4 kb[NT2], kg[NT2], kt[NT2];
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            if (g.bo) kb[t] = *(const f32x4 *)(g.bo + n0 + 4 * t);
+            kg[t] = *(const f32x4 *)(g.ga + n0 + 4 * t);
+            kt[t] = *(const f32x4 *)(g.ba + n0 + 4 * t);
+        }
+#pragma unroll
+        for (int tm = 0; tm < MT; ++tm) {
+            const int r = tm * 16 + (lane & 15), row = min(m0 + r, g.M - 1);
+            const f32x2 sa = g.stats_a[row];
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+                const int n = n0 + 4 * t;
+                const f16x4 ya4 = *(const f16x4 *)(g.ya + (size_t)row * HD + n);
+                f32x4 x = acc0[t][tm];
+                if (g.bo) x += kb[t];
+                x += ln_resid_v(ya4, sa, kg[t], kt[t]);
+                f16x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
+                *(f16x4 *)(lds + (n >> 6) * BM * ROWB + r * ROWB + ((((n & 63) >> 3) ^ (lane & 7)) << 4) +
+                           (n & 7) * 2) = o;
+            }
+        }
+        // The attention tile is consumed and yB is complete: the h/c region
+        // takes the fold terms, and the weights of the block proper follow.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        prefetch_w();
+        dma_fold_terms();
+    } else {
+        prefetch_w();
+        dma_tile(g.y, lds0);
+        dma_fold_terms();
+        // Everything above has landed (the weights were requested first, so
+        // their latency overlaps the tile's) and every wave's part is visible.
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    // Everything above has landed (the weights were requested first, so
-    // their latency overlaps the tile's) and every wave's part is visible.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // (mean, rstd) of a tile's rows in row_stats' order: 16 lanes per row,
     // lane l16 holding 16-byte chunks c·16 + l16; each row's result goes to
     // dst(r, stats) from lane 0 of each row.  The conditions are uniform per
@@ -151,16 +232,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
             }
         }
     };
-    if (!g.stats) {
+    if (OUTP || !g.stats) {
         tile_stats(atile, [&](int r, f32x2 st) { lst[r] = st; });
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // (with OUTP also the fold terms and weights requested above)
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-
-    // Fragment offsets inside a 16-row group: row lane%16, logical chunk
-    // lane/16 + 4·(ks%2) at physical chunk ^ (lane%8).
-    int fo[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) fo[k] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * k) ^ (lane & 7)) << 4);
     // Chunk-local phase-1 features of this lane: fl .. fl + 4·NT1 − 1.
     const int fl = wave * 16 * NT1 + (lane >> 4) * 4 * NT1;
 
@@ -336,8 +412,13 @@ int cu_count() {
 template <int MT>
 hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
     const int grid = (g.M + 16 * MT - 1) / (16 * MT);
-    if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true>), dim3(grid), dim3(64 * NW), 0, s, g);
-    else hipLaunchKernelGGL((mlp_kernel<MT, false>), dim3(grid), dim3(64 * NW), 0, s, g);
+    if (g.attn) {
+        if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true, true>), dim3(grid), dim3(64 * NW), 0, s, g);
+        else hipLaunchKernelGGL((mlp_kernel<MT, false, true>), dim3(grid), dim3(64 * NW), 0, s, g);
+    } else {
+        if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true, false>), dim3(grid), dim3(64 * NW), 0, s, g);
+        else hipLaunchKernelGGL((mlp_kernel<MT, false, false>), dim3(grid), dim3(64 * NW), 0, s, g);
+    }
     return hipGetLastError();
 }
 
@@ -360,8 +441,9 @@ bool mlp_ok(int M, int H, int I) {
 }
 
 hipError_t mlp(const MlpArgs &g, hipStream_t s) {
-    if (!mlp_ok(g.M, HD, g.I) || !g.y || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
+    if (!mlp_ok(g.M, HD, g.I) || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
         return hipErrorInvalidValue;
+    if (g.attn ? !g.wo || !g.ya || !g.stats_a || !g.ga || !g.ba || g.stats : !g.y) return hipErrorInvalidValue;
     const int ncu = cu_count();
     if (ncu <= 0) return hipErrorUnknown;
     // Tokens per block: the fewest 16-row tiles that cover M with one block

@@ -95,6 +95,20 @@ int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const flo
               const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
               void *stats_out, float eps, int32_t M, int32_t H, int32_t I, void *stream);
 
+/* The rest of an encoder layer after attention, in one kernel (hidden 384,
+ * GELU): yB = attn·Woᵀ + bo + (ya − mean_a)·rstd_a·ga + ba is built on-chip
+ * (Wo = fh_op_mlp_pack kind 2 of the [384, 384] projection, bo may be NULL,
+ * stats_a the (mean, rstd) of ya's rows), then out = fh_op_mlp's block of
+ * yB with yB's statistics computed in the kernel.  Gives the same bits as
+ * fh_op_gemm_ln RES_LN for yB followed by fh_op_mlp.  out may alias ya and
+ * stats_out stats_a.
+ * Replaces: native/model.go:596-633 (output projection, residual + norm1, FFN,
+ * residual). */
+int fh_op_outproj_mlp(const void *attn, const void *wo_packed, const float *bo, const void *ya, const void *stats_a,
+                      const float *ga, const float *ba, const void *w1_packed, const float *c1, const float *c2,
+                      const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
+                      void *stats_out, float eps, int32_t M, int32_t H, int32_t I, void *stream);
+
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,
  * holding each sequence's first q_limit=1 query row), f32 or binary16.

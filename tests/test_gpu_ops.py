@@ -342,6 +342,54 @@ def test_mlp_equals_the_two_folded_gemms(M, I, bias):
         np.testing.assert_allclose(got.astype(np.float64), ref, atol=2e-3 * math.sqrt(I) / 4 + 4e-3, rtol=2e-3)
 
 
+@pytest.mark.parametrize("M,bias", [(13, True), (1000, False), (18048, True)])
+def test_outproj_mlp_equals_outproj_then_mlp(M, bias):
+    """The layer tail in one kernel (fh_op_outproj_mlp: the attention output
+    projection with its residual LayerNorm rebuilt, then the feed-forward
+    block) gives the same bits as fh_op_gemm_ln RES_LN followed by fh_op_mlp,
+    with the output statistics, also when the output overwrites ya
+    (native/model.go:596-633)."""
+    H, I, eps = 384, 1536, 1e-12
+    rng = np.random.default_rng(M + 11)
+    attn = rng.standard_normal((M, H)).astype(np.float16)
+    ya = (rng.standard_normal((M, H)) * 2 + 0.3).astype(np.float16)
+    wo = (rng.standard_normal((H, H)) * 0.05).astype(np.float16)
+    w1 = (rng.standard_normal((I, H)) * 0.05).astype(np.float16)
+    w2 = (rng.standard_normal((H, I)) * 0.05).astype(np.float16)
+    bo = rng.standard_normal(H).astype(np.float32) if bias else None
+    ga, ba = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), (0.1 * rng.standard_normal(H)).astype(np.float32)
+    c1 = w1.astype(np.float64).sum(1).astype(np.float32)
+    c2 = rng.standard_normal(I).astype(np.float32)
+    b2 = rng.standard_normal(H).astype(np.float32)
+    lg, lb = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), (0.1 * rng.standard_normal(H)).astype(np.float32)
+    dattn, dya, dwo, dw1, dw2 = dev(attn), dev(ya), dev(wo), dev(w1), dev(w2)
+    dbo = dev(bo) if bias else None
+    dga, dba, dc1, dc2, db2, dlg, dlb = dev(ga), dev(ba), dev(c1), dev(c2), dev(b2), dev(lg), dev(lb)
+    sa = row_stats(dya, eps)
+    wor = torch.empty_like(dwo)
+    assert _lib().fh_op_ring_pack(ptr(dwo), ptr(wor), H, H, None) == 0
+    wom, w1m, w2m = mlp_pack(2, dwo), mlp_pack(1, dw1), mlp_pack(2, dw2)
+    print(f"outproj_mlp M={M} bias={bias}", flush=True)
+    # reference: the projection GEMM, then the block
+    yb = torch.empty((M, H), dtype=torch.float16, device="cuda")
+    gemm_ln(1, 2, dattn, wor, yb, sa, bias=dbo, yr=dya, lg=dga, lb=dba)
+    want = torch.empty((M, H), dtype=torch.float16, device="cuda")
+    want_st = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+    assert _lib().fh_op_mlp(ptr(yb), None, ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
+                            ptr(want), ptr(want_st), eps, M, H, I, None) == 0
+    sync()
+    for inplace in (False, True):
+        y_in, st_in = dya.clone(), sa.clone()
+        out = y_in if inplace else torch.empty((M, H), dtype=torch.float16, device="cuda")
+        so = st_in if inplace else torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+        assert _lib().fh_op_outproj_mlp(ptr(dattn), ptr(wom), ptr(dbo), ptr(y_in), ptr(st_in), ptr(dga), ptr(dba),
+                                        ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
+                                        ptr(out), ptr(so), eps, M, H, I, None) == 0
+        sync()
+        np.testing.assert_array_equal(out.cpu().numpy(), want.cpu().numpy())
+        np.testing.assert_array_equal(so.cpu().numpy(), want_st.cpu().numpy())
+
+
 def test_mlp_rejects_unfit_shapes():
     from futon_amd import _lib as lib
     d = dev(np.zeros((4096,), np.float16))
