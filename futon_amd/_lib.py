@@ -104,7 +104,7 @@ def load():
     L.fh_op_ring_pack.argtypes = [vp, vp, i32, i32, vp]
     L.fh_op_mlp_pack.argtypes = [i32, vp, vp, i32, i32, vp]
     L.fh_op_mlp.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_float, i32, i32, i32, vp]
-    L.fh_op_outproj_mlp.argtypes = [vp] * 16 + [ctypes.c_float, i32, i32, i32, vp]
+    L.fh_op_outproj_mlp.argtypes = [vp] * 16 + [ctypes.c_float, vp, vp, vp, vp, i32, i32, i32, vp]
     L.fh_op_gemm_ln.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.fh_op_row_stats.argtypes = [vp, i32, i32, ctypes.c_float, vp, vp]
     L.fh_op_attention.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, i32, i32, vp]

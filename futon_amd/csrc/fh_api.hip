@@ -334,7 +334,7 @@ int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k
         for (long u = 0; u < (long)n * k / 8; u++) {
             int row, col;
             if (mlp_kind == 1) fh::mlp_w1_unit(u, k, row, col);
-            else fh::mlp_w2_unit(u, row, col);
+            else fh::mlp_w2_unit(u, k, row, col);
             for (int e = 0; e < 8; e++) h[(size_t)u * 8 + e] = f32_to_f16(w[(size_t)row * k + col + e]);
         }
         const int rc = upload(m, (uint16_t **)&d.wm, h.data(), h.size() * 2);
@@ -576,7 +576,8 @@ bool use_mlp(const DevLayer &L, int M, int I) {
 // LayerNorm fold.  out may alias ya and stats_out stats_a (rows belong to
 // one block, which reads them before it writes).
 int mlp_fused(fh_model *m, const DevLayer &L, const f16 *attn, const f16 *ya, const f32x2 *stats_a,
-              const float *ga, const float *ba, int M, f16 *out, f32x2 *stats_out, hipStream_t s) {
+              const float *ga, const float *ba, int M, f16 *out, f32x2 *stats_out, const DevLayer *next,
+              hipStream_t s) {
     const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
     MlpArgs g{};
     g.y = nullptr;
@@ -600,8 +601,15 @@ int mlp_fused(fh_model *m, const DevLayer &L, const f16 *attn, const f16 *ya, co
     g.eps = (float)m->cfg.layer_norm_eps;
     g.M = M;
     g.I = I;
-    const double flops = 4.0 * M * (double)H * I + 2.0 * M * (double)H * H;
-    const double bytes = (double)M * H * 2 * 3 + 2.0 * H * I * 2 + 2.0 * H * H + M * 8.0 + (stats_out ? M * 8.0 : 0.0);
+    if (next) {  // the next layer's QKV projection of out, into m->qkv
+        g.wq = (const f16 *)next->qkv.wm;
+        g.c1q = next->qkv_c1;
+        g.c2q = next->qkv_c2;
+        g.qkv = m->qkv;
+    }
+    const double flops = 4.0 * M * (double)H * I + 2.0 * M * (double)H * H * (next ? 4 : 1);
+    const double bytes = (double)M * H * 2 * 3 + 2.0 * H * I * 2 + 2.0 * H * H * (next ? 4 : 1) + M * 8.0 +
+                         (stats_out ? M * 8.0 : 0.0) + (next ? (double)M * 3 * H * 2 : 0.0);
     Scope sc(m, K_MLP, flops, bytes, s);
     LCHK(fh::mlp(g, s));
     return FH_OK;
@@ -671,7 +679,8 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, nullptr, nullptr, 0.f, H,
                           nullptr, m->x16, s));
     }
-    bool sa_ready = false;  // sA already holds yA's statistics (written by the previous fused block)
+    bool sa_ready = false;   // sA already holds yA's statistics (written by the previous fused kernel)
+    bool qkv_ready = false;  // qkv already holds this layer's projection (ditto)
     for (int li = 0; li < c.num_layers; li++) {
         const DevLayer &L = m->layers[(size_t)li];
         if ((rc = checkpoint(m, b, cp, s))) return rc;
@@ -680,9 +689,10 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const float *bA = li ? m->layers[(size_t)li - 1].n2b : m->emb_b;
 
         // qkv = LN(yA)·Wqkvᵀ + b  (model.go:555)
-        if ((!sa_ready && (rc = row_stats(m, K_STATS, m->x16, T, m->sA, s))) ||
-            (rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
-                            s)))
+        if (!qkv_ready &&
+            ((!sa_ready && (rc = row_stats(m, K_STATS, m->x16, T, m->sA, s))) ||
+             (rc = gemm_lnin(m, K_GEMM_QKV, L.qkv, m->x16, T, L.qkv_c1, L.qkv_c2, m->sA, m->qkv, 3 * H, fh::ACT_NONE,
+                             s))))
             return rc;
 
         // attention (model.go:557-593, 646-701)
@@ -715,17 +725,22 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1;
         const int kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
 
-        sa_ready = false;
+        sa_ready = qkv_ready = false;
         if (use_mlp(L, M, I)) {
             // yB = attn·Woᵀ + b + LN(yA), then the feed-forward block, in one
             // kernel: yB stays on-chip, its statistics are computed there,
             // and (unless this is the last layer) so are the new yA's for the
             // next layer's QKV fold.  The checkpoint between the two
             // (model.go:603) is taken before the launch.
+            // The next layer's QKV projection (over all T rows, also for the
+            // CLS-pooled last layer) runs at the end of the same kernel.
+            const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
+            if (next && !next->qkv.wm) next = nullptr;
             if ((rc = checkpoint(m, b, cp, s)) ||
-                (rc = mlp_fused(m, L, (const f16 *)m->attn, yA, sA, gA, bA, M, yA, last ? nullptr : m->sA, s)))
+                (rc = mlp_fused(m, L, (const f16 *)m->attn, yA, sA, gA, bA, M, yA, last ? nullptr : m->sA, next, s)))
                 return rc;
             sa_ready = !last;
+            qkv_ready = next != nullptr;
             continue;
         }
         // yB = attn·Woᵀ + b + LN(yA)  (model.go:596-599)
@@ -980,7 +995,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                 (rc = upload(m, &L.qkv_c2, c2.data(), c2.size() * 4)))
                 return bail(rc);
         }
-        if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8, ring_fits(3 * H, H)))) return bail(rc);
+        if ((rc = upload_mat(m, L.qkv, w, 3 * H, H, q8, ring_fits(3 * H, H), mlp_on ? 2 : 0))) return bail(rc);
         if ((rc = ld.vec_f32(nm("attn.qkv.bias"), 3 * H, &L.qkv_b, true))) return bail(rc);
         if ((rc = ld.mat_host(nm("attn.out.weight"), H, H, w)) ||
             (rc = upload_mat(m, L.out, w, H, H, q8, ring_fits(H, H), mlp_on ? 2 : 0)))

@@ -67,6 +67,12 @@ struct MlpArgs {
     const f16 *ya;             // [M, 384] un-normalized input of the attention block's LayerNorm
     const f32x2 *stats_a;      // [M] (mean, rstd) of ya's rows
     const float *ga, *ba;      // [384] γ, β of that LayerNorm
+    // Optional QKV projection of the next layer after the block (wq
+    // non-null): qkv = f16(rstd·(out·Wq'ᵀ − mean·c1q) + c2q) with out's own
+    // statistics (the LN_IN fold of the QKV GEMM).
+    const f16 *wq;             // [1152, 384] γ-scaled, fragment-ordered (mlp_w2_unit)
+    const float *c1q, *c2q;    // [1152]
+    f16 *qkv;                  // [M, 1152]
     float eps;                 // LayerNorm epsilon of both statistics
     int M, I;
 };
@@ -130,11 +136,16 @@ __host__ __device__ inline void mlp_w1_unit(long u, int K, int &row, int &col) {
     row = grp * 16 * MLP_NT1 + 4 * MLP_NT1 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3);
     col = ks * 32 + (l >> 4) * 8;
 }
-// fc2 [384, I]: per 128-column chunk j, wave w (16·NT2 output rows), k-step
-// ks, tile t: f = ((j·NW + w)·4 + ks)·NT2 + t; MFMA row 16t + 4a + e of a
-// wave's rows is its row 4·NT2·a + 4t + e, so each lane ends with 4·NT2
-// consecutive outputs.
-__host__ __device__ inline void mlp_w2_unit(long u, int &row, int &col) {
+// fc2 [384, I] (and each 384-row block of a taller matrix, one after the
+// other: the output projection, the next layer's QKV): per 128-column chunk
+// j, wave w (16·NT2 output rows), k-step ks, tile t:
+// f = ((j·NW + w)·4 + ks)·NT2 + t; MFMA row 16t + 4a + e of a wave's rows
+// is its row 4·NT2·a + 4t + e, so each lane ends with 4·NT2 consecutive
+// outputs.
+__host__ __device__ inline void mlp_w2_unit(long u, int K, int &row, int &col) {
+    const long ub = 384L * K / 8;  // units per 384-row block
+    const int blk = (int)(u / ub);
+    u -= blk * ub;
     const int l = (int)(u & 63);
     long f = u >> 6;
     const int t = (int)(f % MLP_NT2);
@@ -143,11 +154,11 @@ __host__ __device__ inline void mlp_w2_unit(long u, int &row, int &col) {
     f /= 4;
     const int w = (int)(f % MLP_NW), j = (int)(f / MLP_NW);
     const int p = 16 * t + (l & 15);
-    row = 16 * MLP_NT2 * w + 4 * MLP_NT2 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3);
+    row = 384 * blk + 16 * MLP_NT2 * w + 4 * MLP_NT2 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3);
     col = j * 128 + ks * 32 + (l >> 4) * 8;
 }
 // out = the fragment-ordered copy of B [N, K]: kind 1 (fc1, K % 32 == 0,
-// N % (16·MLP_NT1) == 0) or kind 2 (fc2, N == 384, K % 128 == 0).
+// N % (16·MLP_NT1) == 0) or kind 2 (N % 384 == 0, K % 128 == 0).
 hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s);
 // Whether mlp() takes an M-row problem with intermediate width I.
 bool mlp_ok(int M, int H, int I);

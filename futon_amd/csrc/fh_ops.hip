@@ -120,7 +120,7 @@ extern "C" int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, v
 
 extern "C" int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N, int32_t K, void *stream) {
     if (!B || !out || N <= 0 || K <= 0) return FH_EINVAL;
-    if (kind == 1 ? N % 16 || K % 32 : kind != 2 || N != 384 || K % 128) return FH_EINVAL;
+    if (kind == 1 ? N % 16 || K % 32 : kind != 2 || N % 384 || K % 128) return FH_EINVAL;
     return code_of(fh::mlp_pack(kind, (const f16 *)B, (f16 *)out, N, K, (hipStream_t)stream));
 }
 
@@ -152,7 +152,8 @@ extern "C" int fh_op_outproj_mlp(const void *attn, const void *wo_packed, const 
                                  const void *stats_a, const float *ga, const float *ba, const void *w1_packed,
                                  const float *c1, const float *c2, const void *w2_packed, const float *b2,
                                  const float *ln_g, const float *ln_b, void *out, void *stats_out, float eps,
-                                 int32_t M, int32_t H, int32_t I, void *stream) {
+                                 const void *wq_packed, const float *c1q, const float *c2q, void *qkv, int32_t M,
+                                 int32_t H, int32_t I, void *stream) {
     if (!attn || !wo_packed || !ya || !stats_a || !ga || !ba || !w1_packed || !c1 || !c2 || !w2_packed || !ln_g ||
         !ln_b || !out || M < 0)
         return FH_EINVAL;
@@ -176,6 +177,10 @@ extern "C" int fh_op_outproj_mlp(const void *attn, const void *wo_packed, const 
     g.out = (f16 *)out;
     g.stats_out = (f32x2 *)stats_out;
     g.eps = eps;
+    g.wq = (const f16 *)wq_packed;
+    g.c1q = c1q;
+    g.c2q = c2q;
+    g.qkv = (f16 *)qkv;
     g.M = M;
     g.I = I;
     return code_of(fh::mlp(g, (hipStream_t)stream));

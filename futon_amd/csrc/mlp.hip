@@ -57,8 +57,11 @@ constexpr int W1C = NW * KS1 * NT1 * 64;  // 16-byte units of W1 per chunk
 constexpr int W2C = NW * KS2 * NT2 * 64;  // 16-byte units of W2 per chunk
 static_assert(CH == NW * 16 * NT1 && NT2 * 16 * NW == HD, "wave split");
 
-template <int MT, bool BIAS, bool OUTP>
+// MODE 0: the block from y; 1: with the output projection ahead of it
+// (OUTP); 2: also with the next layer's QKV projection after it (QKVN).
+template <int MT, bool BIAS, int MODE>
 __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
+    constexpr bool OUTP = MODE >= 1, QKVN = MODE == 2;
     constexpr int BM = 16 * MT;
     constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
     constexpr int H_BYTES = (CH / 64) * BM * ROWB;  // one chunk's h, k-block major
@@ -382,10 +385,70 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
             __builtin_amdgcn_raw_buffer_store_b128(v, rO, (uint32_t)((m0 + r) * HD * 2 + cu * 16), 0, 0);
         }
     }
-    if (g.stats_out)
+    if (g.stats_out || QKVN)
         tile_stats(otile, [&](int r, f32x2 st) {
-            if (m0 + r < g.M) g.stats_out[m0 + r] = st;
+            if (g.stats_out && m0 + r < g.M) g.stats_out[m0 + r] = st;
+            if (QKVN) lst[r] = st;  // every wave has read y's statistics (barrier above)
         });
+    if constexpr (QKVN) {
+        // The next layer's QKV projection of the output tile (the QKV GEMM's
+        // LN_IN form: same K order, same fold arithmetic), 384 columns per
+        // pass; Wq fragments stream through registers four k-steps ahead and
+        // each lane stores its 4·NT2 consecutive columns per token.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const __amdgpu_buffer_rsrc_t rQ = buf_rsrc(g.qkv, (uint32_t)g.M * (3 * HD * 2));
+        const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+            const i32x4 *wqp = (const i32x4 *)g.wq + (size_t)p * (HD * HD / 8) + (size_t)wave * KS2 * NT2 * 64 + lane;
+            i32x4 wqf[KS2][NT2];
+#pragma unroll
+            for (int ks = 0; ks < KS2; ++ks)
+#pragma unroll
+                for (int t = 0; t < NT2; ++t) wqf[ks][t] = wqp[(ks * NT2 + t) * 64];
+            f32x4 kc1[NT2], kc2[NT2];
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+                kc1[t] = *(const f32x4 *)(g.c1q + p * HD + n0 + 4 * t);
+                kc2[t] = *(const f32x4 *)(g.c2q + p * HD + n0 + 4 * t);
+            }
+            f32x4 accq[NT2][MT];
+#pragma unroll
+            for (int k = 0; k < KS1; ++k) {
+                const uint8_t *ab = otile + (k >> 1) * BM * ROWB + fo[k & 1];
+                i32x4 af[MT];
+#pragma unroll
+                for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+#pragma unroll
+                for (int t = 0; t < NT2; ++t) {
+#pragma unroll
+                    for (int tm = 0; tm < MT; ++tm)
+                        accq[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(f16x8, wqf[k % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
+                            k == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : accq[t][tm], 0, 0, 0);
+                    if (k + KS2 < KS1) {
+                        const int kn = k + KS2;
+                        wqf[k % KS2][t] = wqp[(size_t)(kn / KS2) * W2C + ((kn % KS2) * NT2 + t) * 64];
+                    }
+                }
+            }
+#pragma unroll
+            for (int tm = 0; tm < MT; ++tm) {
+                const int r = tm * 16 + (lane & 15);
+                const f32x2 sv = lst[r];
+#pragma unroll
+                for (int t = 0; t < NT2; ++t) {
+                    const f32x4 x = ln_fold_v(accq[t][tm], sv, kc1[t], kc2[t]);
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rQ,
+                                                          (uint32_t)(((m0 + r) * 3 * HD + p * HD + n0 + 4 * t) * 2), 0,
+                                                          0);
+                }
+            }
+        }
+    }
 }
 
 // out = the fragment-ordered copy of B, 16 bytes per thread.
@@ -394,7 +457,7 @@ __global__ void mlp_pack_kernel(int kind, const f16 *__restrict__ B, f16 *__rest
     if (u >= (long)N * K / 8) return;
     int row, col;
     if (kind == 1) fh::mlp_w1_unit(u, K, row, col);
-    else fh::mlp_w2_unit(u, row, col);
+    else fh::mlp_w2_unit(u, K, row, col);
     *(f16x8 *)(out + u * 8) = *(const f16x8 *)(B + (size_t)row * K + col);
 }
 
@@ -412,12 +475,14 @@ int cu_count() {
 template <int MT>
 hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
     const int grid = (g.M + 16 * MT - 1) / (16 * MT);
-    if (g.attn) {
-        if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true, true>), dim3(grid), dim3(64 * NW), 0, s, g);
-        else hipLaunchKernelGGL((mlp_kernel<MT, false, true>), dim3(grid), dim3(64 * NW), 0, s, g);
-    } else {
-        if (g.b2) hipLaunchKernelGGL((mlp_kernel<MT, true, false>), dim3(grid), dim3(64 * NW), 0, s, g);
-        else hipLaunchKernelGGL((mlp_kernel<MT, false, false>), dim3(grid), dim3(64 * NW), 0, s, g);
+    const int mode = g.attn ? (g.wq ? 2 : 1) : 0;
+    switch (mode * 2 + (g.b2 ? 1 : 0)) {
+    case 0: hipLaunchKernelGGL((mlp_kernel<MT, false, 0>), dim3(grid), dim3(64 * NW), 0, s, g); break;
+    case 1: hipLaunchKernelGGL((mlp_kernel<MT, true, 0>), dim3(grid), dim3(64 * NW), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((mlp_kernel<MT, false, 1>), dim3(grid), dim3(64 * NW), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((mlp_kernel<MT, true, 1>), dim3(grid), dim3(64 * NW), 0, s, g); break;
+    case 4: hipLaunchKernelGGL((mlp_kernel<MT, false, 2>), dim3(grid), dim3(64 * NW), 0, s, g); break;
+    default: hipLaunchKernelGGL((mlp_kernel<MT, true, 2>), dim3(grid), dim3(64 * NW), 0, s, g); break;
     }
     return hipGetLastError();
 }
@@ -427,7 +492,7 @@ hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
 namespace fh {
 
 hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s) {
-    if (N <= 0 || K <= 0 || !(kind == 1 ? N % (16 * NT1) == 0 && K % 32 == 0 : kind == 2 && N == HD && K % CH == 0))
+    if (N <= 0 || K <= 0 || !(kind == 1 ? N % (16 * NT1) == 0 && K % 32 == 0 : kind == 2 && N % HD == 0 && K % CH == 0))
         return hipErrorInvalidValue;
     const long n = (long)N * (K / 8);
     hipLaunchKernelGGL(mlp_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kind, B, out, N, K);
@@ -444,6 +509,8 @@ hipError_t mlp(const MlpArgs &g, hipStream_t s) {
     if (!mlp_ok(g.M, HD, g.I) || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
         return hipErrorInvalidValue;
     if (g.attn ? !g.wo || !g.ya || !g.stats_a || !g.ga || !g.ba || g.stats : !g.y) return hipErrorInvalidValue;
+    if (g.wq && (!g.attn || !g.c1q || !g.c2q || !g.qkv || (double)g.M * 3 * HD * 2 >= 2147483648.0))
+        return hipErrorInvalidValue;
     const int ncu = cu_count();
     if (ncu <= 0) return hipErrorUnknown;
     // Tokens per block: the fewest 16-row tiles that cover M with one block

@@ -73,10 +73,11 @@ int fh_op_ring_pack(const void *B, void *out, int32_t N, int32_t K, void *stream
  * unit u holds row r, columns c .. c+7 with lane l = u % 64 taking row
  * l % 16 of its tile and columns 8·(l/16) ..).  kind 1 (fc1 [I, 384], N % 16
  * == 0, K % 32 == 0): fragment f = u / 64 is 16-row tile f / (K/32), k-step
- * f % (K/32).  kind 2 (fc2 [384, I], K % 128 == 0): f = ((8j + w)·4 + ks)·3 +
- * t for 128-column chunk j, 48-row group w, k-step ks, tile t, and MFMA row
- * 16t + 4g + e of a group is row 12g + 4t + e.  No reference counterpart (a
- * layout of this build). */
+ * f % (K/32).  kind 2 (fc2 [384, I] and any [384·n, K], K % 128 == 0; each
+ * 384-row block packed in turn): f = ((8j + w)·4 + ks)·3 + t for 128-column
+ * chunk j, 48-row group w, k-step ks, tile t, and MFMA row 16t + 4g + e of a
+ * group is row 12g + 4t + e.  No reference counterpart (a layout of this
+ * build). */
 int fh_op_mlp_pack(int32_t kind, const void *B, void *out, int32_t N, int32_t K, void *stream);
 
 /* The encoder layer's feed-forward block in one kernel, hidden width H = 384,
@@ -99,15 +100,18 @@ int fh_op_mlp(const void *y, const void *stats, const void *w1_packed, const flo
  * GELU): yB = attn·Woᵀ + bo + (ya − mean_a)·rstd_a·ga + ba is built on-chip
  * (Wo = fh_op_mlp_pack kind 2 of the [384, 384] projection, bo may be NULL,
  * stats_a the (mean, rstd) of ya's rows), then out = fh_op_mlp's block of
- * yB with yB's statistics computed in the kernel.  Gives the same bits as
- * fh_op_gemm_ln RES_LN for yB followed by fh_op_mlp.  out may alias ya and
- * stats_out stats_a.
+ * yB with yB's statistics computed in the kernel.  With wq_packed (kind 2 of
+ * the next layer's γ-scaled [1152, 384] QKV weights) it also writes
+ * qkv [M, 1152] = the LN_IN fold of out with c1q/c2q and out's statistics.
+ * Gives the same bits as fh_op_gemm_ln RES_LN for yB, fh_op_mlp, then
+ * fh_op_gemm_ln LN_IN for qkv.  out may alias ya and stats_out stats_a.
  * Replaces: native/model.go:596-633 (output projection, residual + norm1, FFN,
- * residual). */
+ * residual) and the next layer's QKV projection (:555). */
 int fh_op_outproj_mlp(const void *attn, const void *wo_packed, const float *bo, const void *ya, const void *stats_a,
                       const float *ga, const float *ba, const void *w1_packed, const float *c1, const float *c2,
                       const void *w2_packed, const float *b2, const float *ln_g, const float *ln_b, void *out,
-                      void *stats_out, float eps, int32_t M, int32_t H, int32_t I, void *stream);
+                      void *stats_out, float eps, const void *wq_packed, const float *c1q, const float *c2q, void *qkv,
+                      int32_t M, int32_t H, int32_t I, void *stream);
 
 /* Multi-head attention over packed sequences: qkv [T, 3H] binary16 (q | k | v,
  * heads-major), offsets [nseq+1].  Output [T, H] (or [nseq, H] when compact,

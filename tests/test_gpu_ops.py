@@ -256,11 +256,14 @@ def mlp_units(kind, N, K):
     lane, f = u % 64, u // 64
     if kind == 1:
         return (f // (K // 32)) * 16 + lane % 16, (f % (K // 32)) * 32 + (lane // 16) * 8
+    blk = u // (384 * K // 8)
+    f = (u % (384 * K // 8)) // 64
     t, f = f % 3, f // 3
     ks, f = f % 4, f // 4
     w, j = f % 8, f // 8
     p = 16 * t + lane % 16
-    return 48 * w + 12 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3), j * 128 + ks * 32 + (lane // 16) * 8
+    return (384 * blk + 48 * w + 12 * ((p >> 2) & 3) + 4 * (p >> 4) + (p & 3),
+            j * 128 + ks * 32 + (lane // 16) * 8)
 
 
 def mlp_pack(kind, d):
@@ -270,7 +273,7 @@ def mlp_pack(kind, d):
     return out
 
 
-@pytest.mark.parametrize("kind,N,K", [(1, 1536, 384), (1, 48, 64), (2, 384, 1536), (2, 384, 128)])
+@pytest.mark.parametrize("kind,N,K", [(1, 1536, 384), (1, 48, 64), (2, 384, 1536), (2, 384, 128), (2, 1152, 384)])
 def test_mlp_pack_is_the_documented_layout(kind, N, K):
     rng = np.random.default_rng(N + K)
     w = rng.standard_normal((N, K)).astype(np.float16)
@@ -378,16 +381,31 @@ def test_outproj_mlp_equals_outproj_then_mlp(M, bias):
     assert _lib().fh_op_mlp(ptr(yb), None, ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
                             ptr(want), ptr(want_st), eps, M, H, I, None) == 0
     sync()
-    for inplace in (False, True):
+    # the next layer's QKV projection of the block's output (LN_IN fold)
+    wq = (rng.standard_normal((3 * H, H)) * 0.05).astype(np.float16)
+    dwq = dev(wq)
+    c1q = wq.astype(np.float64).sum(1).astype(np.float32)
+    c2q = rng.standard_normal(3 * H).astype(np.float32)
+    dc1q, dc2q = dev(c1q), dev(c2q)
+    wqr = torch.empty_like(dwq)
+    assert _lib().fh_op_ring_pack(ptr(dwq), ptr(wqr), 3 * H, H, None) == 0
+    wqm = mlp_pack(2, dwq)
+    want_q = torch.empty((M, 3 * H), dtype=torch.float16, device="cuda")
+    gemm_ln(1, 1, want, wqr, want_q, want_st, 0, dc1q, dc2q)
+    for inplace, with_qkv in ((False, False), (True, False), (False, True), (True, True)):
         y_in, st_in = dya.clone(), sa.clone()
         out = y_in if inplace else torch.empty((M, H), dtype=torch.float16, device="cuda")
         so = st_in if inplace else torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+        qkv = torch.empty((M, 3 * H), dtype=torch.float16, device="cuda") if with_qkv else None
+        q_args = (ptr(wqm), ptr(dc1q), ptr(dc2q), ptr(qkv)) if with_qkv else (None, None, None, None)
         assert _lib().fh_op_outproj_mlp(ptr(dattn), ptr(wom), ptr(dbo), ptr(y_in), ptr(st_in), ptr(dga), ptr(dba),
                                         ptr(w1m), ptr(dc1), ptr(dc2), ptr(w2m), ptr(db2), ptr(dlg), ptr(dlb),
-                                        ptr(out), ptr(so), eps, M, H, I, None) == 0
+                                        ptr(out), ptr(so), eps, *q_args, M, H, I, None) == 0
         sync()
         np.testing.assert_array_equal(out.cpu().numpy(), want.cpu().numpy())
         np.testing.assert_array_equal(so.cpu().numpy(), want_st.cpu().numpy())
+        if with_qkv:
+            np.testing.assert_array_equal(qkv.cpu().numpy(), want_q.cpu().numpy())
 
 
 def test_mlp_rejects_unfit_shapes():
