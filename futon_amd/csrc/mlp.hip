@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     // lane l16 holding 16-byte chunks c·16 + l16; each row's result goes to
     // dst(r, stats) from lane 0 of each row.  The conditions are uniform per
     // wave (BM % 4 == 0).
-    auto tile_stats = [&](const uint8_t *tile, auto dst) {
+    auto tile_stats = [&](const uint8_t *tile, int lane, auto dst) {
         const int l16 = lane & 15;
 #pragma unroll
         for (int r0 = 0; r0 < BM; r0 += NW * 4) {
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         }
     };
     if (OUTP || !g.stats) {
-        tile_stats(atile, [&](int r, f32x2 st) { lst[r] = st; });
+        tile_stats(atile, lane, [&](int r, f32x2 st) { lst[r] = st; });
         // (with OUTP also the fold terms and weights requested above)
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
@@ -341,6 +341,28 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         if (j + 1 < nchunk) chunk(j + 1, accB, accA);
     }
 
+    // The next layer's Wq fragments (k-step kg of the 3·KS1-step stream over
+    // the three 384-row blocks, tile t), the first four requested now so
+    // their latency overlaps the output stage.
+    const i32x4 *wqp = (const i32x4 *)g.wq + (size_t)wave * KS2 * NT2 * 64 + lane;
+    auto wq_frag = [&](int kg, int t) {
+        const int p = kg / KS1, k = kg - p * KS1;
+        return wqp[(size_t)p * (HD * HD / 8) + (size_t)(k / KS2) * W2C + ((k % KS2) * NT2 + t) * 64];
+    };
+    i32x4 wqf[KS2][NT2];
+    if constexpr (QKVN) {
+#pragma unroll
+        for (int ks = 0; ks < KS2; ++ks)
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) wqf[ks][t] = wq_frag(ks, t);
+    }
+
+    {
+    // The lane id again, opaque to the compiler: the output stage recomputes
+    // its LDS offsets instead of keeping the prologue's identical ones alive
+    // (in spill slots) across the chunk loop.
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
     // Output epilogue: acc + b2 + (y − mean)·rstd·γ + β, rounded once; y read
     // back from the resident token tile.  This lane's outputs:
     // n0 = 16·NT2·wave + 4·NT2·(lane/16) + {0 .. 4·NT2 − 1}.  The binary16
@@ -386,26 +408,22 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         }
     }
     if (g.stats_out || QKVN)
-        tile_stats(otile, [&](int r, f32x2 st) {
+        tile_stats(otile, lane, [&](int r, f32x2 st) {
             if (g.stats_out && m0 + r < g.M) g.stats_out[m0 + r] = st;
             if (QKVN) lst[r] = st;  // every wave has read y's statistics (barrier above)
         });
     if constexpr (QKVN) {
         // The next layer's QKV projection of the output tile (the QKV GEMM's
         // LN_IN form: same K order, same fold arithmetic), 384 columns per
-        // pass; Wq fragments stream through registers four k-steps ahead and
-        // each lane stores its 4·NT2 consecutive columns per token.
+        // pass.  The three passes are one stream of 3·KS1 k-steps for the Wq
+        // ring (four k-steps ahead, its first fragments requested before the
+        // output epilogue), so a pass's epilogue overlaps the next pass's
+        // loads; each lane stores its 4·NT2 consecutive columns per token.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const __amdgpu_buffer_rsrc_t rQ = buf_rsrc(g.qkv, (uint32_t)g.M * (3 * HD * 2));
         const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
-            const i32x4 *wqp = (const i32x4 *)g.wq + (size_t)p * (HD * HD / 8) + (size_t)wave * KS2 * NT2 * 64 + lane;
-            i32x4 wqf[KS2][NT2];
-#pragma unroll
-            for (int ks = 0; ks < KS2; ++ks)
-#pragma unroll
-                for (int t = 0; t < NT2; ++t) wqf[ks][t] = wqp[(ks * NT2 + t) * 64];
             f32x4 kc1[NT2], kc2[NT2];
 #pragma unroll
             for (int t = 0; t < NT2; ++t) {
@@ -415,6 +433,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
             f32x4 accq[NT2][MT];
 #pragma unroll
             for (int k = 0; k < KS1; ++k) {
+                const int kg = p * KS1 + k;  // position in the stream
                 const uint8_t *ab = otile + (k >> 1) * BM * ROWB + fo[k & 1];
                 i32x4 af[MT];
 #pragma unroll
@@ -424,12 +443,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
 #pragma unroll
                     for (int tm = 0; tm < MT; ++tm)
                         accq[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, wqf[k % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
+                            __builtin_bit_cast(f16x8, wqf[kg % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
                             k == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : accq[t][tm], 0, 0, 0);
-                    if (k + KS2 < KS1) {
-                        const int kn = k + KS2;
-                        wqf[k % KS2][t] = wqp[(size_t)(kn / KS2) * W2C + ((kn % KS2) * NT2 + t) * 64];
-                    }
+                    if (kg + KS2 < 3 * KS1) wqf[kg % KS2][t] = wq_frag(kg + KS2, t);
                 }
             }
 #pragma unroll
@@ -448,6 +464,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
                 }
             }
         }
+    }
     }
 }
 
