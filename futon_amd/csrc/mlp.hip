@@ -65,10 +65,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     constexpr int BM = 16 * MT;
     constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
     constexpr int H_BYTES = (CH / 64) * BM * ROWB;  // one chunk's h, k-block major
-    constexpr int C_OFF = A_BYTES + 2 * H_BYTES;    // c1 [I_MAX] then c2 [I_MAX] (f32)
-    // After the chunk loop the h/c region holds the output tile (same layout
-    // as the token tile) for the row statistics and coalesced stores.
-    constexpr int O_OFF = A_BYTES, S_OFF = A_BYTES + (2 * H_BYTES + 2 * I_MAX * 4 > A_BYTES ? 2 * H_BYTES + 2 * I_MAX * 4 : A_BYTES);
+    // LDS: the token tile; region R, holding the attention tile (phase 0),
+    // then the two h buffers (the chunk loop), then the output tile (same
+    // layout as the token tile); the fold terms c1/c2, staged at entry; the
+    // row statistics.
+    constexpr int O_OFF = A_BYTES, R_BYTES = 2 * H_BYTES > A_BYTES ? 2 * H_BYTES : A_BYTES;
+    constexpr int C_OFF = A_BYTES + R_BYTES;        // c1 [I_MAX] then c2 [I_MAX] (f32)
+    constexpr int S_OFF = C_OFF + 2 * I_MAX * 4;
     constexpr int TS = MT;                          // epilogue tiles done beside phase 2 (all)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S_OFF + BM * 8];
     const uint8_t *const atile = lds;
@@ -143,17 +146,38 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     if constexpr (OUTP) {
         // Phase 0, the attention output projection (the out-projection GEMM's
         // RES_LN form, same K order and epilogue arithmetic): the attention
-        // tile goes to the h/c region, Wo fragments stream through registers
-        // four k-steps ahead, and yB = attn·Woᵀ + bo + LN_a(ya) is written in
+        // tile goes to region R, Wo fragments stream through registers four
+        // k-steps ahead, and yB = attn·Woᵀ + bo + LN_a(ya) is written in
         // binary16 into the token tile.  This lane's outputs: the same
-        // n0 + {0..4·NT2−1} as the final epilogue.
+        // n0 + {0..4·NT2−1} as the final epilogue.  Everything the phase
+        // reads from memory (the tile, the first Wo fragments, ya and its
+        // statistics, bo/γ/β) and the fold terms for later are requested
+        // before the first wait, so their latencies overlap.
         dma_tile(g.attn, lds0 + O_OFF);
+        dma_fold_terms();
         const i32x4 *w0p = (const i32x4 *)g.wo + (size_t)wave * KS2 * NT2 * 64 + lane;
         i32x4 w0f[KS2][NT2];
 #pragma unroll
         for (int ks = 0; ks < KS2; ++ks)
 #pragma unroll
             for (int t = 0; t < NT2; ++t) w0f[ks][t] = w0p[(ks * NT2 + t) * 64];
+        const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
+        f32x4 kb[NT2], kg[NT2], kt[NT2];
+        f16x4 ya4[MT][NT2];
+        f32x2 sa[MT];
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            if (g.bo) kb[t] = *(const f32x4 *)(g.bo + n0 + 4 * t);
+            kg[t] = *(const f32x4 *)(g.ga + n0 + 4 * t);
+            kt[t] = *(const f32x4 *)(g.ba + n0 + 4 * t);
+        }
+#pragma unroll
+        for (int tm = 0; tm < MT; ++tm) {
+            const int row = min(m0 + tm * 16 + (lane & 15), g.M - 1);
+            sa[tm] = g.stats_a[row];
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) ya4[tm][t] = *(const f16x4 *)(g.ya + (size_t)row * HD + n0 + 4 * t);
+        }
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         f32x4 acc0[NT2][MT];
 #pragma unroll
@@ -175,25 +199,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
                 }
             }
         }
-        const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
-        f32x4 kb[NT2], kg[NT2], kt[NT2];
-#pragma unroll
-        for (int t = 0; t < NT2; ++t) {
-            if (g.bo) kb[t] = *(const f32x4 *)(g.bo + n0 + 4 * t);
-            kg[t] = *(const f32x4 *)(g.ga + n0 + 4 * t);
-            kt[t] = *(const f32x4 *)(g.ba + n0 + 4 * t);
-        }
 #pragma unroll
         for (int tm = 0; tm < MT; ++tm) {
-            const int r = tm * 16 + (lane & 15), row = min(m0 + r, g.M - 1);
-            const f32x2 sa = g.stats_a[row];
+            const int r = tm * 16 + (lane & 15);
 #pragma unroll
             for (int t = 0; t < NT2; ++t) {
                 const int n = n0 + 4 * t;
-                const f16x4 ya4 = *(const f16x4 *)(g.ya + (size_t)row * HD + n);
                 f32x4 x = acc0[t][tm];
                 if (g.bo) x += kb[t];
-                x += ln_resid_v(ya4, sa, kg[t], kt[t]);
+                x += ln_resid_v(ya4[tm][t], sa[tm], kg[t], kt[t]);
                 f16x4 o;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
@@ -201,11 +215,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
                            (n & 7) * 2) = o;
             }
         }
-        // The attention tile is consumed and yB is complete: the h/c region
-        // takes the fold terms, and the weights of the block proper follow.
+        // yB is complete; the weights of the block proper follow.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         prefetch_w();
-        dma_fold_terms();
     } else {
         prefetch_w();
         dma_tile(g.y, lds0);
