@@ -260,7 +260,11 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
         if (max_len <= 128) return launch_d<D, 1, 1, 128>(a, nseq, max_len, out_f32, rope, s);
         return launch_d<D, 1, 1, 64>(a, nseq, max_len, out_f32, rope, s);
     }
-    // Short sequences: one block covers every query and stages K/V once.
+    // Up to 64 tokens: 64 query rows per block (2 waves x 2 tiles); smaller
+    // blocks keep more of them resident (18 us vs 24 us for 512 sequences
+    // of 16..64 tokens at 12 heads of 32).
+    if (max_len <= 64) return launch_d<D, 2, 2, 128>(a, nseq, max_len, out_f32, rope, s);
+    // Up to 128 tokens: one block covers every query and stages K/V once.
     if (max_len <= 128) return launch_d<D, 4, 2, 128>(a, nseq, max_len, out_f32, rope, s);
     return launch_d<D, 4, 1, 64>(a, nseq, max_len, out_f32, rope, s);
 }
