@@ -28,8 +28,9 @@ __device__ __forceinline__ float gelu_erf(float x) {
     q = fmaf(q, t, -0.14224837f);
     q = fmaf(q, t, 0.12741480f);
     const float e = __builtin_amdgcn_exp2f((x * x) * -0.72134752f);
-    const float h = x * (q * t) * e;  // ½·x·erfc(|x|/√2)
-    return x < 0.f ? h : x - h;
+    // h = ½·x·erfc(|x|/√2) = x·(q·t)·e has the sign of x, so x·Φ(x), which is
+    // h for x < 0 and x − h otherwise, is max(x, 0) − |x·q·t|·e.
+    return fmaf(-fabsf(x * (q * t)), e, fmaxf(x, 0.f));
 }
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 

@@ -30,6 +30,7 @@
 // ring GEMM's LN_IN/GELU and RES_LN forms, so the result has the same bits as
 // the two separate GEMMs.
 #include <algorithm>
+#include <type_traits>
 
 #include "fh_common.h"
 #include "gemm_epi.h"
@@ -60,7 +61,7 @@ static_assert(CH == NW * 16 * NT1 && NT2 * 16 * NW == HD, "wave split");
 // MODE 0: the block from y; 1: with the output projection ahead of it
 // (OUTP); 2: also with the next layer's QKV projection after it (QKVN).
 template <int MT, bool BIAS, int MODE>
-__global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void mlp_kernel(MlpArgs g) {
     constexpr bool OUTP = MODE >= 1, QKVN = MODE == 2;
     constexpr int BM = 16 * MT;
     constexpr int A_BYTES = KB1 * BM * ROWB;        // token tile, k-block major
@@ -261,19 +262,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
 #pragma unroll
         for (int t = 0; t < NT2; ++t) acc2[t][tm] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // Phase 1, k-step ks: acc (+)= W1 fragments · y_tileᵀ (ks 0 starts at 0).
-    auto p1_step = [&](int ks, f32x4(&acc)[NT1][MT]) {
+    // Token fragments of phase-1 k-step ks, and h fragments of phase-2
+    // k-step ks from h buffer hb: one b128 per 16-token tile.
+    auto load_af = [&](i32x4(&f)[MT], int ks) {
         const uint8_t *ab = atile + (ks >> 1) * BM * ROWB + fo[ks & 1];
-        i32x4 af[MT];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+        for (int t = 0; t < MT; ++t) f[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+    };
+    auto load_hf = [&](i32x4(&f)[MT], const uint8_t *hb, int ks) {
+        const uint8_t *hr = hb + (ks >> 1) * BM * ROWB + fo[ks & 1];
 #pragma unroll
-        for (int tn = 0; tn < NT1; ++tn)
-#pragma unroll
-            for (int tm = 0; tm < MT; ++tm)
-                acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8, w1f[ks % W1H][tn]), __builtin_bit_cast(f16x8, af[tm]),
-                    ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[tn][tm], 0, 0, 0);
+        for (int t = 0; t < MT; ++t) f[t] = *(const i32x4 *)(hr + t * 16 * ROWB);
     };
     // Phase-1 epilogue of token tile tm of chunk c (acc holds its finished
     // product): fold, GELU, binary16, into h buffer c % 2 at this lane's
@@ -296,13 +295,32 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         else *(f16x4 *)dst = *(const f16x4 *)o;
     };
 
+    // Phase 1 of chunk c into acc (W1 fragments · token tileᵀ), refilling W1
+    // with the fragments half a chunk ahead.  The token fragments of k-step
+    // ks + 1 are requested before the products of k-step ks (register double
+    // buffer; the scheduling barrier keeps that order): this stage has no
+    // other work to cover the LDS latency.
+    auto p1_chunk = [&](int c, f32x4(&acc)[NT1][MT]) {
+        i32x4 af[2][MT];
+        load_af(af[0], 0);
+#pragma unroll
+        for (int ks = 0; ks < KS1; ++ks) {
+            if (ks + 1 < KS1) load_af(af[(ks + 1) & 1], ks + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tn = 0; tn < NT1; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < MT; ++tm)
+                    acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(f16x8, w1f[ks % W1H][tn]), __builtin_bit_cast(f16x8, af[ks & 1][tm]),
+                        ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[tn][tm], 0, 0, 0);
+            w1_refill(c, ks);
+        }
+    };
+
     // Chunk 0's phase 1 and the first part of its epilogue; its W1 registers
     // are refilled with chunk 1's fragments.
-#pragma unroll
-    for (int ks = 0; ks < KS1; ++ks) {
-        p1_step(ks, accA);
-        w1_refill(0, ks);
-    }
+    p1_chunk(0, accA);
 #pragma unroll
     for (int tm = 0; tm < TS; ++tm) epi1_tm(tm, accA, 0);
 
@@ -311,16 +329,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
     // (accC); one barrier; stage B multiplies chunk j's phase 2 (refilling W2
     // with chunk j+1's) beside the first part of chunk j+1's epilogue.  h is
     // double-buffered: chunk j+1's h goes to the buffer chunk j−1 used, read
-    // by every wave before it passed this chunk's barrier.
-    auto chunk = [&](int j, f32x4(&accC)[NT1][MT], f32x4(&accN)[NT1][MT]) {
-        const bool more = j + 1 < nchunk;
-        if (more) {
-#pragma unroll
-            for (int ks = 0; ks < KS1; ++ks) {
-                p1_step(ks, accN);
-                if (TS + ks < MT) epi1_tm(TS + ks, accC, j);
-                w1_refill(j + 1, ks);
-            }
+    // by every wave before it passed this chunk's barrier.  MORE (compile
+    // time, so neither stage branches): chunk j+1 exists.  In stage B the
+    // epilogue's VALU work is interleaved with the products (one MFMA, then a
+    // share of the epilogue), so that the two overlap.
+    auto chunk = [&](int j, f32x4(&accC)[NT1][MT], f32x4(&accN)[NT1][MT], auto more_c) {
+        constexpr bool MORE = decltype(more_c)::value;
+        if constexpr (MORE) {
+            p1_chunk(j + 1, accN);
         } else {
 #pragma unroll
             for (int tm = TS; tm < MT; ++tm) epi1_tm(tm, accC, j);
@@ -330,10 +346,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
         const size_t next2 = (size_t)min(j + 1, nchunk - 1) * W2C;
 #pragma unroll
         for (int ks = 0; ks < KS2; ++ks) {
-            const uint8_t *hr = hb + (ks >> 1) * BM * ROWB + fo[ks & 1];
             i32x4 hf[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t) hf[t] = *(const i32x4 *)(hr + t * 16 * ROWB);
+            load_hf(hf, hb, ks);
 #pragma unroll
             for (int t = 0; t < NT2; ++t) {
 #pragma unroll
@@ -342,15 +356,39 @@ __global__ __launch_bounds__(64 * NW) void mlp_kernel(MlpArgs g) {
                         __builtin_bit_cast(f16x8, w2f[ks][t]), __builtin_bit_cast(f16x8, hf[tm]), acc2[t][tm], 0, 0, 0);
                 w2f[ks][t] = w2p[next2 + (ks * NT2 + t) * 64];
             }
-            if (more) {
+            if constexpr (MORE) {
 #pragma unroll
                 for (int tm = ks * TS / KS2; tm < (ks + 1) * TS / KS2; ++tm) epi1_tm(tm, accN, j + 1);
+                // One epilogue tile is ~80 VALU instructions: spread them
+                // between the k-step's NT2·MT products (groups of one MFMA and
+                // a share of the VALU work; the counts must be constants).
+                const int ntile = (ks + 1) * TS / KS2 - ks * TS / KS2;
+                if (ntile == 1) {
+#pragma unroll
+                    for (int i = 0; i < NT2 * MT; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+                    }
+                } else if (ntile == 2) {
+#pragma unroll
+                    for (int i = 0; i < NT2 * MT; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 11, 0);
+                    }
+                }
             }
         }
     };
-    for (int j = 0; j < nchunk; j += 2) {
-        chunk(j, accA, accB);
-        if (j + 1 < nchunk) chunk(j + 1, accB, accA);
+    int j = 0;
+    for (; j + 2 < nchunk; j += 2) {
+        chunk(j, accA, accB, std::true_type{});
+        chunk(j + 1, accB, accA, std::true_type{});
+    }
+    if (j + 1 < nchunk) {
+        chunk(j, accA, accB, std::true_type{});
+        chunk(j + 1, accB, accA, std::false_type{});
+    } else {
+        chunk(j, accA, accB, std::false_type{});
     }
 
     // The next layer's Wq fragments (k-step kg of the 3·KS1-step stream over
