@@ -36,8 +36,10 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(os.path.
 
 # Per-file code-generation options.  attention.hip: keep MFMA results in
 # VGPRs (its softmax reads every score tile right after the MFMA; in AGPRs
-# each element would cost an extra v_accvgpr_read).
-FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# each element would cost an extra v_accvgpr_read), and let fmaxf skip the
+# NaN-quieting copy of each operand (scores are finite or −inf for masked
+# keys, so the results are bit-identical; ~2% faster).
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]}
 
 
 def sources() -> list[str]:
