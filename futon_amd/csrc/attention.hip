@@ -23,9 +23,27 @@
 
 namespace {
 
-template <int D, int WAVES, int QT, int KBLK, bool OUT_F32, bool ROPE>
-__global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
+#ifndef ATTN_ONE_WAVES
+#define ATTN_ONE_WAVES 6
+#endif
+
+// With one key block and 32-wide heads the kernel fits in 80 VGPRs without
+// spills: ask for six waves per SIMD (four at the compiler's own choice of
+// 107 VGPRs), so more of the many short (sequence, head) blocks are resident.
+// Blocks of fewer than four waves are held to fewer per SIMD by their LDS.
+template <int D, int WAVES, bool ONE>
+constexpr int attn_min_waves() { return (ONE && D == 32 && WAVES >= 4) ? ATTN_ONE_WAVES : 1; }
+
+template <int D, int WAVES, int QT, int KBLK, bool OUT_F32, bool ROPE, bool ONE>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(attn_min_waves<D, WAVES, ONE>(), 8)))
+void attn_kernel(AttnArgs a) {
+    // ONE: every sequence fits in one key block (L <= KBLK), so each query
+    // tile is finished (softmax, PV, normalise, store) before the next one
+    // starts and only one tile's output and statistics are live at a time.
+    // The arithmetic is the same as the multi-block path's first block
+    // (running max -inf, running sum 0), so the results are the same bits.
     constexpr int QROWS = 16 * QT * WAVES;
+    constexpr int QS = ONE ? 1 : QT;  // query tiles with live softmax state
     constexpr int KS = D + 8;     // K LDS row stride (halves)
     constexpr int VS = KBLK + 8;  // Vᵀ LDS row stride (halves)
     constexpr int NKT = KBLK / 16;
@@ -95,16 +113,37 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
         }
     }
 
-    f32x4 o[QT][D / 16];
-    float m_run[QT], l_run[QT];
+    f32x4 o[QS][D / 16];
+    float m_run[QS], l_run[QS];
+    auto reset = [&](int st) {
+        m_run[st] = -INFINITY;
+        l_run[st] = 0.f;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        m_run[qt] = -INFINITY;
-        l_run[qt] = 0.f;
+        for (int t = 0; t < D / 16; ++t) o[st][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
 #pragma unroll
-        for (int t = 0; t < D / 16; ++t) o[qt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    }
+    for (int st = 0; st < QS; ++st) reset(st);
     const float sl2 = a.scale_log2e;
+
+    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4] of each tile.
+    auto store = [&](int qt, int st) {
+        const int q = q0 + (wave * QT + qt) * 16 + (lane & 15);
+        if (q >= nq) return;
+        const float inv = 1.0f / l_run[st];
+        const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+            const int dim = t * 16 + (lane >> 4) * 4;
+            if (dim >= d) continue;
+            const f32x4 v = o[st][t] * inv;
+            if (OUT_F32) {
+                *(f32x4 *)((float *)a.out + orow * a.ldo + head * d + dim) = v;
+            } else {
+                const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * d + dim) = h;
+            }
+        }
+    };
 
     for (int kb0 = 0; kb0 < L; kb0 += KBLK) {
         if (kb0 > 0) __syncthreads();  // previous block's K/V fully consumed
@@ -145,6 +184,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
         // mask only on the last tile).
         auto qtile = [&](auto nv_c, int qt) {
             constexpr int NV = decltype(nv_c)::value;
+            const int st = ONE ? 0 : qt;
             constexpr int NC = (NV + 1) / 2;  // 32-key PV chunks
             // Sᵀ tiles: s[kt][i] = score(key kb0 + kt·16 + (lane/16)·4 + i, query lane%16).
             f32x4 s[NV];
@@ -166,8 +206,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
-            const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+            const float m_new = fmaxf(m_run[st], mx * sl2);  // log2-scaled running max
+            const float corr = __builtin_amdgcn_exp2f(m_run[st] - m_new);
             float psum = 0.f;
             f16x8 pf[NC];
 #pragma unroll
@@ -180,10 +220,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
                 }
             psum += __shfl_xor(psum, 16, 64);
             psum += __shfl_xor(psum, 32, 64);
-            l_run[qt] = l_run[qt] * corr + psum;
-            m_run[qt] = m_new;
+            l_run[st] = l_run[st] * corr + psum;
+            m_run[st] = m_new;
 #pragma unroll
-            for (int t = 0; t < D / 16; ++t) o[qt][t] *= corr;
+            for (int t = 0; t < D / 16; ++t) o[st][t] *= corr;
 
             // Oᵀ += Vᵀ·Pᵀ over 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
 #pragma unroll
@@ -194,13 +234,14 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
                     const f16x4 lo = *(const f16x4 *)vrow;
                     const f16x4 hi = *(const f16x4 *)(vrow + 16);
                     const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[qt][t], 0, 0, 0);
+                    o[st][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[st][t], 0, 0, 0);
                 }
             }
         };
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             if (q0 + (wave * QT + qt) * 16 >= nq) continue;  // tile holds no live query (wave-uniform)
+            if (ONE) reset(0);
             static_assert(NKT <= 8, "key tiles per block");
             switch (nkt) {
             case 1: qtile(std::integral_constant<int, 1>{}, qt); break;
@@ -212,43 +253,28 @@ __global__ __launch_bounds__(WAVES * 64) void attn_kernel(AttnArgs a) {
             case 7: if constexpr (NKT >= 7) qtile(std::integral_constant<int, (NKT >= 7 ? 7 : 1)>{}, qt); break;
             default: qtile(std::integral_constant<int, NKT>{}, qt); break;
             }
+            if (ONE) store(qt, 0);
         }
     }
-
-    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4] of each tile.
+    if (!ONE) {
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const int q = q0 + (wave * QT + qt) * 16 + (lane & 15);
-        if (q >= nq) continue;
-        const float inv = 1.0f / l_run[qt];
-        const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
-#pragma unroll
-        for (int t = 0; t < D / 16; ++t) {
-            const int dim = t * 16 + (lane >> 4) * 4;
-            if (dim >= d) continue;
-            const f32x4 v = o[qt][t] * inv;
-            if (OUT_F32) {
-                *(f32x4 *)((float *)a.out + orow * a.ldo + head * d + dim) = v;
-            } else {
-                const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-                *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * d + dim) = h;
-            }
-        }
+        for (int qt = 0; qt < QT; ++qt) store(qt, qt);
     }
 }
 
-template <int D, int WAVES, int QT, int KBLK>
+template <int D, int WAVES, int QT, int KBLK, bool ONE>
 hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
     constexpr int QROWS = 16 * QT * WAVES;
+    if (ONE && max_len > KBLK) return hipErrorInvalidValue;  // one key block must hold every sequence
     const int qmax = min(max_len, a.q_limit);
     dim3 grid((qmax + QROWS - 1) / QROWS, a.H / a.d, nseq);
     dim3 block(WAVES * 64);
     if (out_f32) {
-        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, true, ONE>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, true, false, ONE>), grid, block, 0, s, a);
     } else {
-        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, true, ONE>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<D, WAVES, QT, KBLK, false, false, ONE>), grid, block, 0, s, a);
     }
     return hipGetLastError();
 }
@@ -257,16 +283,16 @@ template <int D>
 hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
     // CLS row only: one wave per (sequence, head).
     if (a.q_limit <= 16) {
-        if (max_len <= 128) return launch_d<D, 1, 1, 128>(a, nseq, max_len, out_f32, rope, s);
-        return launch_d<D, 1, 1, 64>(a, nseq, max_len, out_f32, rope, s);
+        if (max_len <= 128) return launch_d<D, 1, 1, 128, true>(a, nseq, max_len, out_f32, rope, s);
+        return launch_d<D, 1, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
     }
     // Up to 64 tokens: 64 query rows per block (2 waves x 2 tiles); smaller
     // blocks keep more of them resident (18 us vs 24 us for 512 sequences
     // of 16..64 tokens at 12 heads of 32).
-    if (max_len <= 64) return launch_d<D, 2, 2, 128>(a, nseq, max_len, out_f32, rope, s);
+    if (max_len <= 64) return launch_d<D, 2, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
     // Up to 128 tokens: one block covers every query and stages K/V once.
-    if (max_len <= 128) return launch_d<D, 4, 2, 128>(a, nseq, max_len, out_f32, rope, s);
-    return launch_d<D, 4, 1, 64>(a, nseq, max_len, out_f32, rope, s);
+    if (max_len <= 128) return launch_d<D, 4, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
+    return launch_d<D, 4, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
 }
 
 }  // namespace
