@@ -150,6 +150,40 @@ void attn_kernel(AttnArgs a) {
         // Stage only the key rows the MFMAs read: whole 32-key PV chunks
         // that hold a valid key (rows past L repeat the last key: finite).
         const int rows = min(KBLK, (L - kb0 + 31) & ~31);
+        // One key block: each thread owns a fixed set of (key pair, chunk)
+        // items, so all of its K/V loads are issued before the first LDS
+        // store (row indices clamped to the last key instead of branching),
+        // and Vᵀ is written as packed key pairs (32-bit stores).
+        constexpr int CPR = D / 8;               // 16-byte chunks per row
+        constexpr int PAIRS = KBLK / 2 * CPR;    // (key pair, chunk) items
+        constexpr int NP = PAIRS / (WAVES * 64);
+        constexpr bool PAIRED = ONE && PAIRS % (WAVES * 64) == 0 && NP <= 4;
+        if constexpr (PAIRED) {
+            f16x8 k0[NP], k1[NP], v0[NP], v1[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int c = i * WAVES * 64 + tid, p = c / CPR;
+                const int chl = min(c % CPR, chunks - 1);
+                const f16 *r0 = a.qkv + (size_t)(start + min(2 * p, L - 1)) * ld + head * d + chl * 8;
+                const f16 *r1 = a.qkv + (size_t)(start + min(2 * p + 1, L - 1)) * ld + head * d + chl * 8;
+                k0[i] = *(const f16x8 *)(r0 + H);
+                k1[i] = *(const f16x8 *)(r1 + H);
+                v0[i] = *(const f16x8 *)(r0 + 2 * H);
+                v1[i] = *(const f16x8 *)(r1 + 2 * H);
+            }
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int c = i * WAVES * 64 + tid, p = c / CPR, ch = c % CPR;
+                if (2 * p >= rows) continue;  // rows is a multiple of 32: pairs never straddle it
+                const bool live = ch < chunks;
+                const f16x8 ka = live ? k0[i] : z8, kb = live ? k1[i] : z8;
+                const f16x8 va = live ? v0[i] : z8, vb = live ? v1[i] : z8;
+                *(f16x8 *)&Ks[(2 * p) * KS + ch * 8] = ka;
+                *(f16x8 *)&Ks[(2 * p + 1) * KS + ch * 8] = kb;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) *(f16x2 *)&Vt[(ch * 8 + j) * VS + 2 * p] = (f16x2){va[j], vb[j]};
+            }
+        } else
         for (int c = tid; c < rows * (D / 8); c += WAVES * 64) {
             const int r = c / (D / 8), ch = c % (D / 8);
             const int key = min(kb0 + r, L - 1);
