@@ -512,6 +512,7 @@ def rope_tables(n, d, theta):
     (32, 4, [2, 9, 33, 64], True),
     (384, 12, [1, 16, 63, 64, 65, 128], False),
     (384, 12, [1, 7, 40, 64], True),
+    (384, 12, [300, 5, 129, 64], False),
     (768, 12, [3, 50, 64, 17], False),
     (768, 12, [512, 77], False),
     (768, 12, [300, 700], True),
