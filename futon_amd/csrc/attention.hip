@@ -23,6 +23,9 @@
 
 namespace {
 
+#ifndef ATTN_PAIR_ORDER
+#define ATTN_PAIR_ORDER 1
+#endif
 #ifndef ATTN_ONE_WAVES
 #define ATTN_ONE_WAVES 6
 #endif
@@ -52,9 +55,9 @@ void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
 
     // Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
-    // contiguous range of (sequence, head, query group) in that order: all
-    // heads of a sequence then share one L2, which fetches the sequence's
-    // qkv rows once instead of once per XCD.
+    // contiguous range of items, ordered so that blocks which read the same
+    // qkv lines share one L2 (the lines are then fetched once, not once per
+    // XCD).
     int seq, head, qg;
     {
         const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * gridDim.z;
@@ -63,8 +66,18 @@ void attn_kernel(AttnArgs a) {
         const int logical = xcd * q8 + min(xcd, r8) + idx;
         qg = logical % gx;
         const int t = logical / gx;
-        head = t % gy;
-        seq = t / gy;
+        if (ATTN_PAIR_ORDER && (gy & 1) == 0) {
+            // (head pair, sequence, head) order: the two heads whose q/k/v
+            // segments share 128-byte lines stay on one XCD, and each XCD's
+            // range spans many sequences, so per-XCD work varies less than
+            // with whole sequences per XCD.
+            const int nseq = gridDim.z, u = t >> 1;
+            head = (u / nseq) * 2 + (t & 1);
+            seq = u % nseq;
+        } else {
+            head = t % gy;
+            seq = t / gy;
+        }
     }
     const int start = a.offsets[seq];
     const int L = a.offsets[seq + 1] - start;
