@@ -30,13 +30,18 @@ EXPORTED = (
     "fh_profile_reset", "fh_profile_read", "fh_debug_cancel_after", "fh_checkpoints_per_call",
     "fh_strerror", "fh_last_error", "fh_model_device_bytes",
     "fh_op_gemm", "fh_op_gemm_ring", "fh_op_gemm_ln", "fh_op_row_stats", "fh_op_ring_pack", "fh_op_mlp_pack", "fh_op_mlp", "fh_op_outproj_mlp", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
-    "fh_op_pool",
+    "fh_op_pool", "fh_route_flags",
     "fh_tokenizer_new", "fh_tokenizer_encode", "fh_tokenizer_vocab_size", "fh_tokenizer_free",
     "fh_pack_load", "fh_pack_config_load", "fh_pack_config", "fh_pack_model_id", "fh_pack_tensor_count",
     "fh_pack_create_model", "fh_pack_free", "fh_safetensors_check",
     "fh_provider_new", "fh_provider_embed", "fh_provider_embed_batch", "fh_provider_dimensions",
     "fh_provider_model_name", "fh_provider_is_available", "fh_provider_close", "fh_provider_free", "fh_futon_new",
 )
+
+
+# FH_ROUTE_* (include/futon_hip_ops.h)
+FH_ROUTE_RING_QKV, FH_ROUTE_RING_OUT, FH_ROUTE_RING_FFN1, FH_ROUTE_RING_FC2 = 1, 2, 4, 8
+FH_ROUTE_MLP, FH_ROUTE_MLP_QKV = 16, 32
 
 
 class FhConfig(ctypes.Structure):
@@ -112,6 +117,8 @@ def load():
     L.fh_op_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
     L.fh_op_embed_ln.argtypes = [vp, vp, i32, i32, vp, vp, vp, vp, vp, ctypes.c_float, i32, vp, vp, vp]
     L.fh_op_pool.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    L.fh_route_flags.restype = i32
+    L.fh_route_flags.argtypes = [i32, i32, i32, i32]
     cp, sz, pvp = ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(vp)
     L.fh_tokenizer_new.argtypes = [cp, ctypes.POINTER(FhTokenizerConfig), pvp]
     L.fh_tokenizer_encode.argtypes = [vp, cp, sz, i32, vp, i32, ctypes.POINTER(i32)]

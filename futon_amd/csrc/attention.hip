@@ -326,11 +326,13 @@ hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
     return hipGetLastError();
 }
 
+static_assert(fh::ATTN_ONE_BLOCK_KEYS == 128, "the one-block kernels stage 128 keys");
+
 template <int D>
 hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
     // CLS row only: one wave per (sequence, head).
     if (a.q_limit <= 16) {
-        if (max_len <= 128) return launch_d<D, 1, 1, 128, true>(a, nseq, max_len, out_f32, rope, s);
+        if (max_len <= fh::ATTN_ONE_BLOCK_KEYS) return launch_d<D, 1, 1, 128, true>(a, nseq, max_len, out_f32, rope, s);
         return launch_d<D, 1, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
     }
     // Up to 64 tokens: 64 query rows per block (2 waves x 2 tiles); smaller
@@ -338,7 +340,7 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
     // of 16..64 tokens at 12 heads of 32).
     if (max_len <= 64) return launch_d<D, 2, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
     // Up to 128 tokens: one block covers every query and stages K/V once.
-    if (max_len <= 128) return launch_d<D, 4, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
+    if (max_len <= fh::ATTN_ONE_BLOCK_KEYS) return launch_d<D, 4, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
     return launch_d<D, 4, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
 }
 

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "../../include/futon_hip.h"
+#include "../../include/futon_hip_ops.h"
 #include "fh_common.h"
 #include "host/host_common.h"
 
@@ -113,8 +114,15 @@ struct DevMat {
 
 // The persistent ring GEMM pays off once its tiles cover about half the
 // CUs; fewer rows (small batches, the CLS-pooled last layer) run on the
-// tiled GEMM's smaller tiles with the natural-order copy.
-bool use_ring(const DevMat &w, int M) { return w.wr && fh::gemm_ring_worth(M, w.n); }
+// tiled GEMM's smaller tiles with the natural-order copy.  The ring also
+// addresses its operands with 32-bit buffer offsets: a problem whose rows
+// overflow them (gemm_ring_ok) runs on the 64-bit-indexed tiled GEMM, with
+// the same bits.
+bool use_ring(const DevMat &w, const GemmArgs &g, int act, bool out_f32, int ln) {
+    if (!w.wr || !fh::gemm_ring_worth(g.M, w.n)) return false;
+    if (act == fh::ACT_NONE && !out_f32 && g.resid_h && !g.resid) act = fh::ACT_RES16;  // as gemm_ring does
+    return fh::gemm_ring_ok(g, act, out_f32, ln);
+}
 
 struct DevLayer {
     DevMat qkv, out, ffn1, fc2;  // ffn1 = fc1, or fc1|gate interleaved in 16-row blocks (SwiGLU)
@@ -169,9 +177,19 @@ struct fh_model {
     int32_t *ids = nullptr, *offsets = nullptr;
     f32x2 *sA = nullptr, *sB = nullptr, *sAc = nullptr, *sBc = nullptr;  // per-row (mean, rstd)
     f16 *yBc = nullptr;
-    // Pinned host staging for fh_encode.
+    // fh_encode's batch I/O (ids in schedule order, per-chunk offsets, the
+    // vectors): device buffer and pinned host staging of the same layout.
+    void *io = nullptr;
+    size_t io_bytes = 0;
     void *pin = nullptr;
     size_t pin_bytes = 0;
+    int chunk_tokens = 1 << 18;  // most tokens one fh_encode chunk runs in one forward
+    // Every forward is ordered after the previous one, whatever stream each
+    // ran on: done_ev is recorded at the end of each forward (done_stream is
+    // where), and the next forward's stream waits on it.  Synchronizing
+    // done_ev therefore drains every earlier use of the workspace.
+    hipEvent_t done_ev = nullptr;
+    hipStream_t done_stream = nullptr;
 
     std::mutex mu;
     int cancel_after = -1;
@@ -382,6 +400,45 @@ int eff_max_len(const fh_config &c) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Waits for every forward enqueued so far on any stream (they are chained
+// through done_ev) and for the model's own stream.
+hipError_t drain(fh_model *m) {
+    hipError_t e = hipSuccess;
+    if (m->done_stream) e = hipEventSynchronize(m->done_ev);
+    const hipError_t e2 = hipStreamSynchronize(m->stream);
+    return e != hipSuccess ? e : e2;
+}
+
+// A forward on stream s starts after the previous forward ends (which may
+// have run on another stream) ...
+int begin_on(fh_model *m, hipStream_t s) {
+    if (m->done_stream && !(s == m->stream && m->done_stream == m->stream))
+        HIPCHK(hipStreamWaitEvent(s, m->done_ev, 0));
+    return FH_OK;
+}
+// ... and marks its own end.
+int end_on(fh_model *m, hipStream_t s) {
+    HIPCHK(hipEventRecord(m->done_ev, s));
+    m->done_stream = s;
+    return FH_OK;
+}
+
+// fh_encode's I/O buffers, device and pinned host, `bytes` each.
+int ensure_io(fh_model *m, size_t bytes) {
+    if (bytes <= m->io_bytes && bytes <= m->pin_bytes) return FH_OK;
+    HIPCHK(drain(m));
+    if (m->io) HIPCHK(hipFree(m->io));
+    if (m->pin) HIPCHK(hipHostFree(m->pin));
+    m->io = m->pin = nullptr;
+    m->io_bytes = m->pin_bytes = 0;
+    hipError_t e = hipMalloc(&m->io, bytes);
+    if (e != hipSuccess) return fail(FH_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    e = hipHostMalloc(&m->pin, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) return fail(FH_ENOMEM, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    m->io_bytes = m->pin_bytes = bytes;
+    return FH_OK;
+}
+
 int ensure_workspace(fh_model *m, int tokens, int seqs) {
     if (tokens <= m->cap_tokens && seqs <= m->cap_seqs) return FH_OK;
     const int T = std::max(tokens, m->cap_tokens), S = std::max(seqs, m->cap_seqs);
@@ -410,9 +467,10 @@ int ensure_workspace(fh_model *m, int tokens, int seqs) {
         off += align256(p.second);
     }
     if (m->ws) {
-        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(drain(m));
         HIPCHK(hipFree(m->ws));
         m->ws = nullptr;
+        m->cap_tokens = m->cap_seqs = 0;
     }
     hipError_t e = hipMalloc(&m->ws, off);
     if (e != hipSuccess) return fail(FH_ENOMEM, "workspace hipMalloc(%zu): %s", off, hipGetErrorString(e));
@@ -468,6 +526,38 @@ void drain_profile(fh_model *m) {
     m->pending.clear();
 }
 
+// Cancellation checkpoints observed while the forward executes: at each
+// checkpoint an event marks the work enqueued so far, and the host waits
+// until the GPU has finished the work before checkpoint k − kPaceAhead
+// before it reads the cancel flag and enqueues more.  The GPU keeps up to
+// kPaceAhead half-layers queued, so pacing costs it no idle time, and a
+// flag raised at any moment during the forward is seen at the next
+// checkpoint the GPU reaches (model.go:400, :603 check between layers as
+// they run).
+constexpr int kPaceAhead = 2;
+struct Pacer {
+    std::vector<hipEvent_t> ev;  // one per checkpoint passed, in order
+    size_t done = 0;             // checkpoints whose preceding work has finished
+};
+
+hipEvent_t take_event(fh_model *m) {
+    if (m->event_pool.empty()) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+        return e;
+    }
+    hipEvent_t e = m->event_pool.back();
+    m->event_pool.pop_back();
+    return e;
+}
+
+void release_pacer(fh_model *m, Pacer &p) {
+    for (hipEvent_t e : p.ev)
+        if (e) m->event_pool.push_back(e);
+    p.ev.clear();
+    p.done = 0;
+}
+
 struct BatchInfo {
     const int32_t *d_ids, *d_offsets;
     int nseq, T, max_len, out_dim;
@@ -475,6 +565,8 @@ struct BatchInfo {
     double sum_l2 = 0.0;  // Σ L_i², for attention FLOP accounting
     const volatile int32_t *cancel = nullptr;
     bool host_checks = false;  // cancellation checkpoints active
+    Pacer *pacer = nullptr;    // non-null: pace the enqueue against execution
+    int *cp_base = nullptr;    // running checkpoint count across the call's chunks
 };
 
 #define LCHK(expr)                                                                         \
@@ -484,8 +576,15 @@ struct BatchInfo {
     } while (0)
 
 int checkpoint(fh_model *m, const BatchInfo &b, int &cp, hipStream_t s) {
-    const int idx = cp++;
+    const int idx = (b.cp_base ? *b.cp_base : 0) + cp++;
     if (!b.host_checks) return FH_OK;
+    if (Pacer *p = b.pacer) {
+        hipEvent_t e = take_event(m);
+        if (!e) return fail(FH_EHIP, "hipEventCreate failed");
+        p->ev.push_back(e);
+        LCHK(hipEventRecord(e, s));
+        while (p->ev.size() - p->done > (size_t)kPaceAhead) LCHK(hipEventSynchronize(p->ev[p->done++]));
+    }
     const bool hit = (b.cancel && *b.cancel != 0) || (m->cancel_after >= 0 && idx == m->cancel_after);
     if (hit) {
         hipStreamSynchronize(s);
@@ -519,7 +618,7 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
                          (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : resid_h ? (double)M * outn * 2 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    const bool ring = use_ring(w, M);
+    const bool ring = !i8 && use_ring(w, g, act, out_f32, fh::LN_NONE);
     if (ring) g.B = w.wr;
     LCHK(ring ? fh::gemm_ring(g, act, out_f32, s) : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
     return FH_OK;
@@ -555,7 +654,7 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
     const int outn = act == fh::ACT_SWIGLU ? w.n / 2 : w.n;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * outn * 2 + M * 8.0;
     Scope sc(m, cls, flops, bytes, s);
-    const bool ring = use_ring(w, M);
+    const bool ring = use_ring(w, g, act, false, fh::LN_IN);
     if (ring) g.B = w.wr;
     LCHK(ring ? fh::gemm_ring(g, act, false, s, fh::LN_IN) : fh::gemm_f16(g, act, false, s, fh::LN_IN));
     return FH_OK;
@@ -564,8 +663,9 @@ int gemm_lnin(fh_model *m, int cls, const DevMat &w, const f16 *y, int M, const 
 // Whether layer L's output projection and feed-forward block run fused for
 // M rows: the fragment-ordered copies exist and M is large enough for the
 // ring-sized path.
-bool use_mlp(const DevLayer &L, int M, int I) {
-    return L.fc2.wm && L.ffn1.wm && L.out.wm && fh::gemm_ring_worth(M, I) && fh::mlp_ok(M, L.fc2.n, I);
+bool use_mlp(const DevLayer &L, int M, int I, bool with_qkv) {
+    return L.fc2.wm && L.ffn1.wm && L.out.wm && fh::gemm_ring_worth(M, I) && fh::mlp_ok(M, L.fc2.n, I) &&
+           (!with_qkv || fh::mlp_qkv_ok(M));
 }
 
 // The rest of the layer after attention in one kernel (fh::mlp with the
@@ -639,7 +739,7 @@ int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, cons
     const double flops = 2.0 * M * (double)w.n * w.k;
     const double bytes = (double)M * w.k * 2 + (double)w.n * w.k * 2 + (double)M * w.n * 4 + M * 8.0;
     Scope sc(m, cls, flops, bytes, s);
-    const bool ring = use_ring(w, M);
+    const bool ring = use_ring(w, g, fh::ACT_NONE, false, fh::RES_LN);
     if (ring) g.B = w.wr;
     LCHK(ring ? fh::gemm_ring(g, fh::ACT_NONE, false, s, fh::RES_LN) : fh::gemm_f16(g, fh::ACT_NONE, false, s, fh::RES_LN));
     return FH_OK;
@@ -726,7 +826,9 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
 
         sa_ready = qkv_ready = false;
-        if (use_mlp(L, M, I)) {
+        const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
+        if (next && !next->qkv.wm) next = nullptr;
+        if (use_mlp(L, M, I, next != nullptr)) {
             // yB = attn·Woᵀ + b + LN(yA), then the feed-forward block, in one
             // kernel: yB stays on-chip, its statistics are computed there,
             // and (unless this is the last layer) so are the new yA's for the
@@ -734,10 +836,9 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             // (model.go:603) is taken before the launch.
             // The next layer's QKV projection (over all T rows, also for the
             // CLS-pooled last layer) runs at the end of the same kernel.
-            const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
-            if (next && !next->qkv.wm) next = nullptr;
             if ((rc = checkpoint(m, b, cp, s)) ||
-                (rc = mlp_fused(m, L, (const f16 *)m->attn, yA, sA, gA, bA, M, yA, last ? nullptr : m->sA, next, s)))
+                (rc = mlp_fused(m, L, (const f16 *)(last_cls ? m->attnc : m->attn), yA, sA, gA, bA, M, yA,
+                                last ? nullptr : m->sA, next, s)))
                 return rc;
             sa_ready = !last;
             qkv_ready = next != nullptr;
@@ -898,8 +999,13 @@ extern "C" void fh_model_destroy(fh_model *m) {
         hipEventDestroy(p.b);
     }
     for (auto e : m->event_pool) hipEventDestroy(e);
+    if (m->done_ev) {
+        if (m->done_stream) hipEventSynchronize(m->done_ev);
+        hipEventDestroy(m->done_ev);
+    }
     for (void *p : m->allocs) hipFree(p);
     if (m->ws) hipFree(m->ws);
+    if (m->io) hipFree(m->io);
     if (m->pin) hipHostFree(m->pin);
     if (m->stream) hipStreamDestroy(m->stream);
     delete m;
@@ -936,6 +1042,11 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     m->device = device;
     m->hd = hd;
     m->eff_max = eff_max_len(c);
+    if (const char *ct = getenv("FUTON_CHUNK_TOKENS")) {
+        const long v = strtol(ct, nullptr, 10);
+        if (v > 0 && v < INT_MAX) m->chunk_tokens = (int)v;
+    }
+    m->chunk_tokens = std::max(m->chunk_tokens, m->eff_max);  // a chunk always holds the longest sequence
     int rc = FH_OK;
     auto bail = [&](int code) {
         fh_model_destroy(m);
@@ -943,6 +1054,8 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     };
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
         return bail(fail(FH_EHIP, "hipStreamCreate failed"));
+    if (hipEventCreateWithFlags(&m->done_ev, hipEventDisableTiming) != hipSuccess)
+        return bail(fail(FH_EHIP, "hipEventCreate failed"));
 
     Loader ld{m, tensors, n_tensors, std::vector<bool>((size_t)n_tensors, false)};
     if ((rc = ld.mat_f32("embeddings.word", c.vocab_size, H, &m->word))) return bail(rc);
@@ -1102,8 +1215,6 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
     const fh_config &c = m->cfg;
     if (seq_offsets[0] != 0) return fail(FH_EINVAL, "native: seq_offsets[0] must be 0");
     // Per-sequence validation in the reference's order (model.go:348-365).
-    int max_len = 0;
-    double sum_l2 = 0.0;
     for (int i = 0; i < nseq; i++) {
         const int L = seq_offsets[i + 1] - seq_offsets[i];
         if (L <= 0) return fail(FH_EINVAL, "native: batch item %d: native: empty token sequence", i);
@@ -1123,43 +1234,106 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
                 return fail(FH_EINVAL, "native: batch item %d: native: token id %d outside vocab of %d", i, ids[t],
                             c.vocab_size);
         }
-        max_len = std::max(max_len, L);
-        sum_l2 += (double)L * L;
     }
     const int T = seq_offsets[nseq];
     const int od = out_dim == 0 ? c.hidden_size : out_dim;
 
+    // Schedule (the batch counterpart of the reference's longest-first
+    // dispatch, provider.go:183-246): sequences sorted longest first, cut
+    // into chunks that each hold one attention class — every sequence fits
+    // one key block (≤ fh::ATTN_ONE_BLOCK_KEYS keys), or none does — and at
+    // most chunk_tokens tokens.  Each chunk is one packed forward, so a long
+    // sequence does not move the short ones onto the multi-block attention
+    // path, and a sequence's vector (computed in a fixed order by kernels
+    // chosen only by its own class) is the same bits in any batch.
+    std::vector<int> ord((size_t)nseq);
+    for (int i = 0; i < nseq; i++) ord[(size_t)i] = i;
+    auto len = [&](int i) { return seq_offsets[i + 1] - seq_offsets[i]; };
+    std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return len(a) > len(b); });
+    struct Chunk {
+        int s0, ns, t0, nt, max_len;
+        double sum_l2;
+    };
+    std::vector<Chunk> chunks;
+    int max_nt = 0, max_ns = 0;
+    {
+        int t = 0;
+        for (int j = 0; j < nseq; j++) {
+            const int L = len(ord[(size_t)j]);
+            const bool one = L <= fh::ATTN_ONE_BLOCK_KEYS;
+            if (chunks.empty() || (chunks.back().max_len <= fh::ATTN_ONE_BLOCK_KEYS) != one ||
+                chunks.back().nt + L > m->chunk_tokens)
+                chunks.push_back({j, 0, t, 0, L, 0.0});
+            Chunk &k = chunks.back();
+            k.ns++;
+            k.nt += L;
+            k.sum_l2 += (double)L * L;
+            t += L;
+            max_nt = std::max(max_nt, k.nt);
+            max_ns = std::max(max_ns, k.ns);
+        }
+    }
+    const int nch = (int)chunks.size();
+    // I/O layout: ids in schedule order | chunk-local offsets (ns + 1 per
+    // chunk) | vectors in schedule order.
+    const size_t off_ids = 0, off_offs = align256((size_t)T * 4);
+    const size_t off_out = off_offs + align256((size_t)(nseq + nch) * 4);
+    const size_t io_need = off_out + (size_t)nseq * od * 4;
+
     std::lock_guard<std::mutex> lk(m->mu);
     HIPCHK(hipSetDevice(m->device));
-    int rc = ensure_workspace(m, T, nseq);
+    int rc = ensure_workspace(m, max_nt, max_ns);
+    if (rc || (rc = ensure_io(m, io_need))) return rc;
+    // The staging buffer is free: every earlier forward that read it has
+    // finished (fh_encode waits for its own before returning).
+    int32_t *p_ids = (int32_t *)((char *)m->pin + off_ids), *p_off = (int32_t *)((char *)m->pin + off_offs);
+    const float *p_out = (const float *)((char *)m->pin + off_out);
+    {
+        int32_t *pi = p_ids, *po = p_off;
+        for (const Chunk &k : chunks) {
+            int32_t acc = 0;
+            *po++ = 0;
+            for (int j = k.s0; j < k.s0 + k.ns; j++) {
+                const int i = ord[(size_t)j], L = len(i);
+                memcpy(pi, ids + seq_offsets[i], (size_t)L * 4);
+                pi += L;
+                acc += L;
+                *po++ = acc;
+            }
+        }
+    }
+    hipStream_t s = m->stream;
+    if ((rc = begin_on(m, s))) return rc;
+    char *io = (char *)m->io;
+    HIPCHK(hipMemcpyAsync(io, m->pin, off_out, hipMemcpyHostToDevice, s));
+    // Pace the enqueue against execution only when something can cancel.
+    Pacer pacer;
+    const bool pace = cancel != nullptr || m->cancel_after >= 0;
+    int cp_base = 0;
+    for (int ci = 0; ci < nch && rc == FH_OK; ci++) {
+        const Chunk &k = chunks[(size_t)ci];
+        BatchInfo b{(const int32_t *)(io + off_ids) + k.t0, (const int32_t *)(io + off_offs) + k.s0 + ci, k.ns, k.nt,
+                    k.max_len, out_dim, (float *)(io + off_out) + (size_t)k.s0 * od};
+        b.sum_l2 = k.sum_l2;
+        b.cancel = cancel;
+        b.host_checks = true;
+        b.pacer = pace ? &pacer : nullptr;
+        b.cp_base = &cp_base;
+        rc = run_forward(m, b, s);
+        cp_base += 2 * c.num_layers;
+    }
+    if (rc == FH_OK) {
+        const hipError_t e = hipMemcpyAsync((void *)p_out, io + off_out, (size_t)nseq * od * 4,
+                                            hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) rc = fail(FH_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+    }
+    const int rc_end = end_on(m, s);
+    const hipError_t es = hipStreamSynchronize(s);
+    release_pacer(m, pacer);
     if (rc) return rc;
-    const size_t need = align256((size_t)T * 4) + align256((size_t)(nseq + 1) * 4) + (size_t)nseq * od * 4;
-    if (need > m->pin_bytes) {
-        if (m->pin) HIPCHK(hipHostFree(m->pin));
-        m->pin = nullptr;
-        m->pin_bytes = 0;
-        hipError_t e = hipHostMalloc(&m->pin, need, hipHostMallocDefault);
-        if (e != hipSuccess) return fail(FH_ENOMEM, "hipHostMalloc(%zu): %s", need, hipGetErrorString(e));
-        m->pin_bytes = need;
-    }
-    int32_t *p_ids = (int32_t *)m->pin;
-    int32_t *p_off = (int32_t *)((char *)m->pin + align256((size_t)T * 4));
-    float *p_out = (float *)((char *)p_off + align256((size_t)(nseq + 1) * 4));
-    memcpy(p_ids, ids, (size_t)T * 4);
-    memcpy(p_off, seq_offsets, (size_t)(nseq + 1) * 4);
-    HIPCHK(hipMemcpyAsync(m->ids, p_ids, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
-    HIPCHK(hipMemcpyAsync(m->offsets, p_off, (size_t)(nseq + 1) * 4, hipMemcpyHostToDevice, m->stream));
-    BatchInfo b{m->ids, m->offsets, nseq, T, max_len, out_dim, m->out};
-    b.sum_l2 = sum_l2;
-    b.cancel = cancel;
-    b.host_checks = true;
-    if ((rc = run_forward(m, b, m->stream))) {
-        hipStreamSynchronize(m->stream);
-        return rc;
-    }
-    HIPCHK(hipMemcpyAsync(p_out, m->out, (size_t)nseq * od * 4, hipMemcpyDeviceToHost, m->stream));
-    HIPCHK(hipStreamSynchronize(m->stream));
-    memcpy(out, p_out, (size_t)nseq * od * 4);
+    if (rc_end) return rc_end;
+    if (es != hipSuccess) return fail(FH_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(es));
+    for (int j = 0; j < nseq; j++) memcpy(out + (size_t)ord[(size_t)j] * od, p_out + (size_t)j * od, (size_t)od * 4);
     if (m->prof) drain_profile(m);
     return FH_OK;
 }
@@ -1189,7 +1363,51 @@ extern "C" int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t
     } else {
         b.sum_l2 = (double)total_tokens * max_len;  // upper bound without host offsets
     }
-    return run_forward(m, b, stream ? (hipStream_t)stream : m->stream);
+    hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+    if ((rc = begin_on(m, s))) return rc;
+    rc = run_forward(m, b, s);
+    const int rc_end = end_on(m, s);
+    return rc ? rc : rc_end;
+}
+
+extern "C" int32_t fh_route_flags(int32_t hidden, int32_t inter, int32_t swiglu, int32_t M) {
+    if (hidden <= 0 || inter <= 0 || M <= 0) return 0;
+    const int H = hidden, I = inter;
+    const bool fold = H % 64 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16);
+    if (!fold) return 0;
+    auto mat = [](int n, int k) {
+        DevMat d;
+        d.n = n;
+        d.k = k;
+        d.wr = (n % 128 == 0 && k % 64 == 0) ? (void *)&d : nullptr;  // a stand-in: only its presence is read
+        return d;
+    };
+    auto args = [](int M, int n, int k, int lda, int ldc, bool resid) {
+        GemmArgs g{};
+        g.M = M;
+        g.N = n;
+        g.K = k;
+        g.lda = lda;
+        g.ldb = k;
+        g.ldc = ldc;
+        g.ldr = resid ? ldc : 0;
+        g.resid_h = resid ? (const f16 *)&g : nullptr;  // presence only
+        return g;
+    };
+    int32_t f = 0;
+    const DevMat q = mat(3 * H, H), o = mat(H, H), f1 = mat(swiglu ? 2 * I : I, H), f2 = mat(H, I);
+    if (use_ring(q, args(M, 3 * H, H, H, 3 * H, false), fh::ACT_NONE, false, fh::LN_IN)) f |= FH_ROUTE_RING_QKV;
+    if (use_ring(o, args(M, H, H, H, H, true), fh::ACT_NONE, false, fh::RES_LN)) f |= FH_ROUTE_RING_OUT;
+    if (!swiglu && use_ring(f1, args(M, I, H, H, I, false), fh::ACT_GELU, false, fh::LN_IN)) f |= FH_ROUTE_RING_FFN1;
+    if (use_ring(f2, args(M, H, I, I, H, true), fh::ACT_NONE, false, fh::RES_LN)) f |= FH_ROUTE_RING_FC2;
+    if (!swiglu && fh::mlp_ok(1, H, I) && I % 128 == 0) {
+        DevLayer L;
+        L.fc2.wm = L.ffn1.wm = L.out.wm = (void *)&L;  // presence only
+        L.fc2.n = H;
+        if (use_mlp(L, M, I, false)) f |= FH_ROUTE_MLP;
+        if (use_mlp(L, M, I, true)) f |= FH_ROUTE_MLP_QKV;
+    }
+    return f;
 }
 
 extern "C" int fh_profile_enable(fh_model *m, int32_t on) {

@@ -160,9 +160,17 @@ __host__ __device__ inline void mlp_w2_unit(long u, int K, int &row, int &col) {
 // out = the fragment-ordered copy of B [N, K]: kind 1 (fc1, K % 32 == 0,
 // N % (16·MLP_NT1) == 0) or kind 2 (N % 384 == 0, K % 128 == 0).
 hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s);
-// Whether mlp() takes an M-row problem with intermediate width I.
+// Whether mlp() takes an M-row problem with intermediate width I, and
+// whether it can also write the next layer's Q/K/V for M rows (32-bit
+// buffer offsets into the [M, 1152] output).
 bool mlp_ok(int M, int H, int I);
+bool mlp_qkv_ok(int M);
 hipError_t mlp(const MlpArgs &a, hipStream_t s);
+// Sequences of at most ATTN_ONE_BLOCK_KEYS tokens take attention's
+// one-key-block path (each query tile's softmax over all keys at once);
+// longer ones the multi-block path (64-key blocks, online rescaling).  The
+// two round differently, so a batch that mixes them is split (fh_encode).
+constexpr int ATTN_ONE_BLOCK_KEYS = 128;
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
 // gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
 // binary16 sum to x16 instead, for a consumer that folds this LayerNorm.

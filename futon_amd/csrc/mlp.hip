@@ -572,12 +572,13 @@ bool mlp_ok(int M, int H, int I) {
            (double)I * HD * 2 < 2147483648.0;
 }
 
+bool mlp_qkv_ok(int M) { return M > 0 && (double)M * 3 * HD * 2 < 2147483648.0; }
+
 hipError_t mlp(const MlpArgs &g, hipStream_t s) {
     if (!mlp_ok(g.M, HD, g.I) || !g.w1 || !g.c1 || !g.c2 || !g.w2 || !g.ln_g || !g.ln_b || !g.out)
         return hipErrorInvalidValue;
     if (g.attn ? !g.wo || !g.ya || !g.stats_a || !g.ga || !g.ba || g.stats : !g.y) return hipErrorInvalidValue;
-    if (g.wq && (!g.attn || !g.c1q || !g.c2q || !g.qkv || (double)g.M * 3 * HD * 2 >= 2147483648.0))
-        return hipErrorInvalidValue;
+    if (g.wq && (!g.attn || !g.c1q || !g.c2q || !g.qkv || !mlp_qkv_ok(g.M))) return hipErrorInvalidValue;
     const int ncu = cu_count();
     if (ncu <= 0) return hipErrorUnknown;
     // Tokens per block: the fewest 16-row tiles that cover M with one block

@@ -144,6 +144,22 @@ int fh_op_embed_ln(const int32_t *ids, const int32_t *offsets, int32_t nseq, int
 int fh_op_pool(const float *x32, const int32_t *offsets, int32_t nseq, int32_t H, int32_t cls_compact,
                int32_t matryoshka_ln, int32_t out_dim, int32_t normalize, float *out, void *stream);
 
+/* Which kernels a layer of the binary16 (LayerNorm-folded) forward runs for
+ * M rows of a pack with this hidden width, intermediate width and
+ * activation: FH_ROUTE_* bits (0 = every GEMM on the tiled kernel, or a
+ * width the fold does not cover).  Host-only, no device needed.  A
+ * projection leaves the persistent ring GEMM, and the layer tail the fused
+ * kernel, when its rows no longer fit 32-bit buffer offsets; the tiled GEMM
+ * (64-bit indices) then computes the same bits.  No reference counterpart:
+ * routing diagnostics. */
+#define FH_ROUTE_RING_QKV 1
+#define FH_ROUTE_RING_OUT 2
+#define FH_ROUTE_RING_FFN1 4
+#define FH_ROUTE_RING_FC2 8
+#define FH_ROUTE_MLP 16      /* out projection + FFN fused (last layer) */
+#define FH_ROUTE_MLP_QKV 32  /* ... and the next layer's QKV projection */
+int32_t fh_route_flags(int32_t hidden, int32_t inter, int32_t swiglu, int32_t M);
+
 #ifdef __cplusplus
 }
 #endif

@@ -168,9 +168,17 @@ static inline float reduce8(const float *l) {
     return (v0 + v1) + (v2 + v3);
 }
 
+/* Threads one GEMM splits its 4-row panels over (each output element is
+ * still computed whole by one thread, in the order above): 1 inside
+ * fo_encode_batch's per-sequence workers, all of them when a batch has fewer
+ * sequences than threads (the reference's parallelTiles, kernel.go:106-127,
+ * splits one GEMM the same way without changing any element's order). */
+static int inner_threads = 1;
+
 void fo_matmul_t(float *dst, const float *a, const float *b, int m, int n, int k,
                  const float *bias) {
     const int k8 = k & ~7;
+#pragma omp parallel for schedule(static) num_threads(inner_threads) if (inner_threads > 1 && m >= 32)
     for (int i = 0; i < m; i += 4) {
         const int rows = (m - i) < 4 ? (m - i) : 4;
         const float *ar[4];
@@ -639,6 +647,21 @@ int fo_encode_batch(const fo_model *m, const int32_t *ids, const int32_t *offset
                     int out_dim, float *out, int threads, char *err, int errlen) {
     const int od = out_dim == 0 ? m->cfg.hidden : out_dim;
     int failed = 0;
+    if (threads > 1 && nseq < threads) {
+        /* Fewer sequences than threads (long-context batches): one sequence
+         * at a time, its GEMMs split over the threads. */
+        inner_threads = threads;
+        for (int i = 0; i < nseq && !failed; i++) {
+            char e[256];
+            if (fo_encode(m, ids + offsets[i], offsets[i + 1] - offsets[i], out_dim, out + (size_t)i * od, e,
+                          sizeof e) != 0) {
+                snprintf(err, (size_t)errlen, "native: batch item %d: %s", i, e);
+                failed = 1;
+            }
+        }
+        inner_threads = 1;
+        return failed ? -1 : 0;
+    }
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
     for (int i = 0; i < nseq; i++) {
         char e[256];

@@ -192,3 +192,39 @@ def test_synthetic_pack_is_deterministic(tmp_path):
     assert (ids[off[:-1]] == 101).all() and (ids[off[1:] - 1] == 102).all()
     inner = np.delete(ids, np.concatenate([off[:-1], off[1:] - 1]))
     assert inner.min() >= 1000 and inner.max() <= 30521
+
+
+def test_routing_falls_back_before_32bit_offsets_overflow():
+    """The persistent ring GEMM and the fused layer tail address rows with
+    32-bit buffer offsets.  At the row counts where those offsets would
+    overflow, the forward must route the projection to the tiled GEMM
+    (64-bit indices, same bits) instead of failing; below them it keeps the
+    fast kernels.  Host-only: fh_route_flags evaluates the same predicates
+    run_forward_fold uses."""
+    from futon_amd import _lib
+    L = _lib.load()
+    R = _lib
+    all_ring = R.FH_ROUTE_RING_QKV | R.FH_ROUTE_RING_OUT | R.FH_ROUTE_RING_FFN1 | R.FH_ROUTE_RING_FC2
+    # bge-small / MiniLM (H=384, I=1536, GELU): everything fused at the bench size
+    f = L.fh_route_flags(384, 1536, 0, 18048)
+    assert f & all_ring == all_ring and f & R.FH_ROUTE_MLP and f & R.FH_ROUTE_MLP_QKV
+    # small batches: tiled GEMMs, nothing fused (fewer than 192 ring tiles)
+    assert L.fh_route_flags(384, 1536, 0, 1000) == 0
+    # the fused tail's next-layer Q/K/V ([M, 1152] binary16) overflows at M·2304 ≥ 2^31
+    lim_q = (1 << 31) // (3 * 384 * 2)
+    assert L.fh_route_flags(384, 1536, 0, lim_q) & R.FH_ROUTE_MLP_QKV
+    assert not L.fh_route_flags(384, 1536, 0, lim_q + 1) & R.FH_ROUTE_MLP_QKV
+    assert L.fh_route_flags(384, 1536, 0, lim_q + 1) & R.FH_ROUTE_MLP
+    # the QKV ring GEMM at H=384 writes [M+256, 1152] binary16 rows
+    lim = (1 << 31) // (3 * 384 * 2) - 256
+    assert L.fh_route_flags(384, 1536, 0, lim - 1) & R.FH_ROUTE_RING_QKV
+    assert not L.fh_route_flags(384, 1536, 0, lim + 1) & R.FH_ROUTE_RING_QKV
+    # BERT-base FFN1 (ldc = 3072): ring up to (M+256)·6144 < 2^31
+    lim = (1 << 31) // (3072 * 2) - 256
+    f_ok, f_over = L.fh_route_flags(768, 3072, 0, lim - 1), L.fh_route_flags(768, 3072, 0, lim + 1)
+    assert f_ok & R.FH_ROUTE_RING_FFN1 and not f_over & R.FH_ROUTE_RING_FFN1
+    assert f_over & R.FH_ROUTE_RING_OUT  # the narrower outputs still fit
+    assert not f_ok & R.FH_ROUTE_MLP  # the fused tail is built for hidden 384 only
+    # SwiGLU's interleaved FFN1 always runs tiled; H=32 (toy) is not folded
+    assert not L.fh_route_flags(768, 3072, 1, 65536) & R.FH_ROUTE_RING_FFN1
+    assert L.fh_route_flags(32, 64, 0, 1 << 20) == 0
