@@ -29,7 +29,10 @@ sys.path.insert(0, ROOT)
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 PEAK_I8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
-GEMM_CLASSES = ("gemm_qkv", "gemm_out", "gemm_ffn1", "gemm_fc2")
+# Every kernel class whose FLOPs are GEMM work: the separate projection GEMMs
+# (including the CLS layer's compact ones) and the fused layer tail, which
+# is four GEMMs (output projection, FFN1, FC2, next layer's QKV) in one launch.
+GEMM_CLASSES = ("gemm_qkv", "gemm_out", "gemm_ffn1", "gemm_fc2", "mlp_fused")
 
 
 def parse():
@@ -41,6 +44,10 @@ def parse():
     ap.add_argument("--pack-root", default=os.path.join(tempfile.gettempdir(), "futon_bench_packs"))
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mixed", action="store_true",
+                    help="instead of the throughput line: a batch of 256 sequences of 2..512 tokens through "
+                         "fh_encode, scheduled by attention class (default) against one packed forward "
+                         "(FUTON_SCHEDULE=0), host buffers both ways")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 launches) and exit; its "
                          "FETCH_SIZE/WRITE_SIZE counters calibrate the per-launch traffic figures")
@@ -91,26 +98,98 @@ def flops_per_embedding(cfg: dict, L: int) -> float:
     return N * full
 
 
+def host_cpus():
+    """(usable threads, affinity count, cgroup CPU limit or None, CPU model)."""
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return (min(aff, quota) if quota else aff), aff, quota, model
+
+
 def cpu_baseline(w, cfg, tensors, ids, offsets, target_s: float):
+    """The oracle (the restated reference forward) over a bounded sample of
+    the same batch: on every usable host core, one sequence per thread as the
+    reference's batchPlan runs large batches, and on one thread."""
     import oracle
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
+    threads, aff, quota, model = host_cpus()
     om = oracle.Model(cfg, tensors, q8=w.q8)
     nseq = offsets.size - 1
-    # probe on `threads` sequences, then size the sample to ≈ target_s
-    n0 = min(nseq, threads)
-    t0 = time.perf_counter()
-    om.encode_batch(ids[:offsets[n0]], offsets[:n0 + 1], w.out_dim, threads)
-    dt = time.perf_counter() - t0
-    n = int(min(nseq, max(n0, n0 * target_s / max(dt, 1e-3))))
-    t0 = time.perf_counter()
-    om.encode_batch(ids[:offsets[n]], offsets[:n + 1], w.out_dim, threads)
-    dt = time.perf_counter() - t0
+
+    def rate(nthreads, budget):
+        # probe on nthreads sequences, then size the sample to ≈ budget seconds
+        n0 = min(nseq, nthreads)
+        t0 = time.perf_counter()
+        om.encode_batch(ids[:offsets[n0]], offsets[:n0 + 1], w.out_dim, nthreads)
+        dt = time.perf_counter() - t0
+        n = int(min(nseq, max(n0, n0 * budget / max(dt, 1e-3))))
+        t0 = time.perf_counter()
+        om.encode_batch(ids[:offsets[n]], offsets[:n + 1], w.out_dim, nthreads)
+        dt = time.perf_counter() - t0
+        return n / dt, n, dt
+
+    v_all, n_all, dt_all = rate(threads, target_s)
+    v_one, n_one, dt_one = rate(1, target_s / 2)
     om.close()
-    return {"value": round(n / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
-            "sample": f"first {n} of the {nseq} sequences of the same batch, oracle/oracle.c "
-                      f"(restated reference forward, AVX2-order GEMM) on {threads} OpenMP threads, "
-                      f"one sequence per thread as the reference's batchPlan at large batch; {dt:.2f} s"}
+    return {"value": round(v_all, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "value_1thread": round(v_one, 3), "nproc": aff, "cgroup_cpu_limit": quota, "cpu_model": model,
+            "sample": f"first {n_all} of the {nseq} sequences of the same batch on {threads} threads "
+                      f"({dt_all:.2f} s) and the first {n_one} on 1 thread ({dt_one:.2f} s): oracle/oracle.c, "
+                      f"the restated reference forward (AVX2-order GEMM), one sequence per thread as the "
+                      f"reference's batchPlan at large batch; {aff} CPUs in the affinity mask"
+                      + (f", cgroup limit {quota}" if quota else "")}
+
+
+def mixed_bench(args) -> None:
+    """fh_encode over a mixed-length batch: the length-class schedule (one
+    forward per attention class, longest first) against one packed forward
+    of the whole batch.  Prints one JSON line."""
+    from futon_amd import native, synth
+    w = synth.workload(args.workload)
+    pack = synth.ensure_workload_pack(w, args.pack_root)
+    ids, offsets = synth.make_batch(w.ids_seed + 100, 256, 2, 512)
+    sched = native.LoadModel(pack, q8=w.q8)
+    os.environ["FUTON_SCHEDULE"] = "0"
+    try:
+        whole = native.LoadModel(pack, q8=w.q8)
+    finally:
+        del os.environ["FUTON_SCHEDULE"]
+    reps = max(5, args.steps // 2)
+    res = {}
+    for name, m in (("scheduled", sched), ("one_call", whole)):
+        for _ in range(3):
+            out = m.EncodePacked(ids, offsets, w.out_dim)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            m.EncodePacked(ids, offsets, w.out_dim)
+        res[name] = (offsets.size - 1) * reps / (time.perf_counter() - t0)
+        res[name + "_out"] = out
+    a, b = res.pop("scheduled_out"), res.pop("one_call_out")
+    cos = float(np.min((a.astype(np.float64) * b).sum(1) /
+                       (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))))
+    lens = np.diff(offsets)
+    print(json.dumps({"metric": "mixed-length batch through fh_encode (host buffers), embeddings/s",
+                      "workload": f"{w.name}, B=256, L 2..512 (T={int(offsets[-1])}, "
+                                  f"{int((lens <= 128).sum())} sequences of <= 128 tokens)",
+                      "scheduled": round(res["scheduled"], 1), "one_call": round(res["one_call"], 1),
+                      "speedup": round(res["scheduled"] / res["one_call"], 3), "reps": reps,
+                      "min_cos_scheduled_vs_one_call": round(cos, 7)}))
+    sched.close()
+    whole.close()
 
 
 def main():
@@ -121,6 +200,9 @@ def main():
         sys.exit(2)
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.mixed:
+        mixed_bench(args)
         return
     import torch
     from futon_amd import native, synth
@@ -181,8 +263,8 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "per_launch_bytes": pd["bytes"] / pd["launches"], "per_launch_us": round(per_launch_ms * 1e3, 3),
                 "launches_per_step": pd["launches"] // args.steps}
-    gemm_ms = sum(prof[k]["ms"] for k in GEMM_CLASSES)
-    gemm_fl = sum(prof[k]["flops"] for k in GEMM_CLASSES)
+    gemm_ms = sum(prof[k]["ms"] for k in GEMM_CLASSES if k in prof)
+    gemm_fl = sum(prof[k]["flops"] for k in GEMM_CLASSES if k in prof)
     gemm_tf = gemm_fl / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     total_fl = float(sum(flops_per_embedding(cfg, int(L)) for L in lens))
     kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 4), "launches_per_step": v["launches"] // args.steps,
@@ -210,7 +292,9 @@ def main():
                                f"B={nseq}, L {w.len_lo}..{w.len_hi} (T={T} tokens, packed)",
                    "global_batch": nseq, "seq_len": max_len, "parallelism": "single-gpu"},
         "roofline": roof,
-        "gemm_mfma": {"tflops": round(gemm_tf, 1), "frac": round(gemm_tf / (PEAK_I8_TOPS if w.q8 else PEAK_F16_TFLOPS), 4)},
+        "gemm_mfma": {"tflops": round(gemm_tf, 1), "frac": round(gemm_tf / (PEAK_I8_TOPS if w.q8 else PEAK_F16_TFLOPS), 4),
+                      "classes": [k for k in GEMM_CLASSES if prof.get(k, {}).get("launches")],
+                      "ms_per_step": round(gemm_ms / args.steps, 4)},
         "model_tflops": round(total_fl * value / nseq / 1e12, 1),
         "model_mfma_frac": round(total_fl * value / nseq / 1e12 / (PEAK_I8_TOPS if w.q8 else PEAK_F16_TFLOPS), 4),
         "host_buffers_value": round(host_rate, 1),

@@ -136,7 +136,8 @@ struct DevLayer {
 
 enum KClass {
     K_EMBED, K_GEMM_QKV, K_ATTN, K_GEMM_OUT, K_LN, K_GEMM_FFN1, K_GEMM_FC2, K_QUANT, K_GATHER, K_POOL,
-    K_CLS_TAIL,  // last CLS layer after its QKV GEMM: attention for row 0 and every M = nseq launch
+    K_CLS_TAIL,  // last CLS layer: attention for row 0, the CLS-row gather, statistics and norms (its GEMMs
+                 // count in the GEMM classes)
     K_STATS,     // row statistics for the folded LayerNorms
     K_MLP,       // fused FFN1 → GELU → FC2 (fh::mlp)
     K_NCLASS
@@ -169,12 +170,11 @@ struct fh_model {
     int cap_tokens = 0, cap_seqs = 0;
     void *ws = nullptr;
     size_t ws_bytes = 0;
-    float *x32 = nullptr, *y32 = nullptr, *xc32 = nullptr, *out = nullptr;
+    float *x32 = nullptr, *y32 = nullptr, *xc32 = nullptr;
     f16 *x16 = nullptr, *qkv = nullptr, *xc16 = nullptr;
     void *attn = nullptr, *attnc = nullptr, *hbuf = nullptr;
     int8_t *xq = nullptr;
     float *xs = nullptr;
-    int32_t *ids = nullptr, *offsets = nullptr;
     f32x2 *sA = nullptr, *sB = nullptr, *sAc = nullptr, *sBc = nullptr;  // per-row (mean, rstd)
     f16 *yBc = nullptr;
     // fh_encode's batch I/O (ids in schedule order, per-chunk offsets, the
@@ -184,6 +184,8 @@ struct fh_model {
     void *pin = nullptr;
     size_t pin_bytes = 0;
     int chunk_tokens = 1 << 18;  // most tokens one fh_encode chunk runs in one forward
+    bool schedule = true;        // sort and split fh_encode batches by attention class (FUTON_SCHEDULE=0: one
+                                 // forward in batch order, for comparison)
     // Every forward is ordered after the previous one, whatever stream each
     // ran on: done_ev is recorded at the end of each forward (done_stream is
     // where), and the next forward's stream waits on it.  Synchronizing
@@ -439,43 +441,69 @@ int ensure_io(fh_model *m, size_t bytes) {
     return FH_OK;
 }
 
-int ensure_workspace(fh_model *m, int tokens, int seqs) {
-    if (tokens <= m->cap_tokens && seqs <= m->cap_seqs) return FH_OK;
-    const int T = std::max(tokens, m->cap_tokens), S = std::max(seqs, m->cap_seqs);
+// The workspace for T tokens and S sequences: each of the model's buffer
+// pointers with its size, in layout order (regions 256-byte aligned).
+// (A fixed-capacity list, so laying out a workspace allocates nothing.)
+struct WsPlan {
+    std::pair<void **, size_t> e[20];
+    int n = 0;
+    const std::pair<void **, size_t> *begin() const { return e; }
+    const std::pair<void **, size_t> *end() const { return e + n; }
+    void push_back(std::pair<void **, size_t> p) { e[n++] = p; }
+};
+WsPlan workspace_plan(fh_model *m, int T, int S) {
     const size_t H = (size_t)m->cfg.hidden_size, I = (size_t)m->cfg.intermediate_size;
     const bool q8 = m->cfg.q8 != 0;
     const size_t hsz = q8 ? 4 : 2;  // FFN hidden / attention output element size
-    size_t off = 0;
-    std::vector<std::pair<void **, size_t>> plan = {
+    WsPlan plan;
+    for (auto p : std::initializer_list<std::pair<void **, size_t>>{
         {(void **)&m->x32, (size_t)T * H * 4},        {(void **)&m->x16, (size_t)T * H * 2},
         {(void **)&m->qkv, (size_t)T * 3 * H * 2},    {(void **)&m->attn, (size_t)T * H * hsz},
         {(void **)&m->y32, (size_t)T * H * 4},        {(void **)&m->hbuf, (size_t)T * I * hsz},
         {(void **)&m->xc32, (size_t)S * H * 4},       {(void **)&m->xc16, (size_t)S * H * 2},
-        {(void **)&m->attnc, (size_t)S * H * hsz},    {(void **)&m->out, (size_t)S * H * 4},
-        {(void **)&m->ids, (size_t)T * 4},            {(void **)&m->offsets, (size_t)(S + 1) * 4},
+        {(void **)&m->attnc, (size_t)S * H * hsz},
         {(void **)&m->sA, (size_t)T * 8},             {(void **)&m->sB, (size_t)T * 8},
         {(void **)&m->sAc, (size_t)S * 8},            {(void **)&m->sBc, (size_t)S * 8},
         {(void **)&m->yBc, (size_t)S * H * 2},
-    };
+    })
+        plan.push_back(p);
     if (q8) {
         plan.push_back({(void **)&m->xq, (size_t)T * std::max(H, I)});
         plan.push_back({(void **)&m->xs, (size_t)T * 4});
     }
-    std::vector<size_t> offs;
+    return plan;
+}
+
+size_t workspace_bytes(const WsPlan &plan) {
+    size_t off = 0;
+    for (auto &p : plan) off += align256(p.second);
+    return off;
+}
+
+// Points the model's buffers into [base, base + workspace_bytes(plan)).
+void carve(const WsPlan &plan, char *base) {
+    size_t off = 0;
     for (auto &p : plan) {
-        offs.push_back(off);
+        *p.first = base + off;
         off += align256(p.second);
     }
+}
+
+int ensure_workspace(fh_model *m, int tokens, int seqs) {
+    if (tokens <= m->cap_tokens && seqs <= m->cap_seqs) return FH_OK;
+    const int T = std::max(tokens, m->cap_tokens), S = std::max(seqs, m->cap_seqs);
+    const auto plan = workspace_plan(m, T, S);
+    const size_t bytes = workspace_bytes(plan);
     if (m->ws) {
         HIPCHK(drain(m));
         HIPCHK(hipFree(m->ws));
         m->ws = nullptr;
         m->cap_tokens = m->cap_seqs = 0;
     }
-    hipError_t e = hipMalloc(&m->ws, off);
-    if (e != hipSuccess) return fail(FH_ENOMEM, "workspace hipMalloc(%zu): %s", off, hipGetErrorString(e));
-    m->ws_bytes = off;
-    for (size_t i = 0; i < plan.size(); i++) *plan[i].first = (char *)m->ws + offs[i];
+    hipError_t e = hipMalloc(&m->ws, bytes);
+    if (e != hipSuccess) return fail(FH_ENOMEM, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    m->ws_bytes = bytes;
+    carve(plan, (char *)m->ws);
     m->cap_tokens = T;
     m->cap_seqs = S;
     return FH_OK;
@@ -822,8 +850,9 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             Scope sc(m, K_CLS_TAIL, 0.0, (double)S * (H * 4 + 16), s);
             LCHK(fh::gather_rows(nullptr, m->x16, m->sA, b.d_offsets, S, H, nullptr, m->xc16, m->sAc, s));
         }
-        const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1;
-        const int kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
+        // The CLS layer's compact (M = nseq) GEMMs count in the GEMM
+        // classes; its attention, gather and statistics in cls_last_layer.
+        const int kOut = K_GEMM_OUT, kFfn1 = K_GEMM_FFN1, kFc2 = K_GEMM_FC2;
 
         sa_ready = qkv_ready = false;
         const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
@@ -935,8 +964,8 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
             LCHK(fh::gather_rows(f32res ? m->x32 : nullptr, f32res ? nullptr : m->x16, nullptr, b.d_offsets, S, H,
                                  f32res ? m->xc32 : nullptr, f32res ? nullptr : m->xc16, nullptr, s));
         }
-        const int kOut = last_cls ? K_CLS_TAIL : K_GEMM_OUT, kLn = last_cls ? K_CLS_TAIL : K_LN;
-        const int kFfn1 = last_cls ? K_CLS_TAIL : K_GEMM_FFN1, kFc2 = last_cls ? K_CLS_TAIL : K_GEMM_FC2;
+        const int kOut = K_GEMM_OUT, kLn = last_cls ? K_CLS_TAIL : K_LN;
+        const int kFfn1 = K_GEMM_FFN1, kFc2 = K_GEMM_FC2;
         const int kQuant = last_cls ? K_CLS_TAIL : K_QUANT;
         const float *r32 = f32res ? xo32 : nullptr;
         const f16 *r16 = f32res ? nullptr : xo16;
@@ -1047,6 +1076,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
         if (v > 0 && v < INT_MAX) m->chunk_tokens = (int)v;
     }
     m->chunk_tokens = std::max(m->chunk_tokens, m->eff_max);  // a chunk always holds the longest sequence
+    if (const char *sc = getenv("FUTON_SCHEDULE")) m->schedule = sc[0] != '0';
     int rc = FH_OK;
     auto bail = [&](int code) {
         fh_model_destroy(m);
@@ -1249,7 +1279,7 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
     std::vector<int> ord((size_t)nseq);
     for (int i = 0; i < nseq; i++) ord[(size_t)i] = i;
     auto len = [&](int i) { return seq_offsets[i + 1] - seq_offsets[i]; };
-    std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return len(a) > len(b); });
+    if (m->schedule) std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return len(a) > len(b); });
     struct Chunk {
         int s0, ns, t0, nt, max_len;
         double sum_l2;
@@ -1261,10 +1291,11 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
         for (int j = 0; j < nseq; j++) {
             const int L = len(ord[(size_t)j]);
             const bool one = L <= fh::ATTN_ONE_BLOCK_KEYS;
-            if (chunks.empty() || (chunks.back().max_len <= fh::ATTN_ONE_BLOCK_KEYS) != one ||
-                chunks.back().nt + L > m->chunk_tokens)
+            if (chunks.empty() || chunks.back().nt + L > m->chunk_tokens ||
+                (m->schedule && (chunks.back().max_len <= fh::ATTN_ONE_BLOCK_KEYS) != one))
                 chunks.push_back({j, 0, t, 0, L, 0.0});
             Chunk &k = chunks.back();
+            k.max_len = std::max(k.max_len, L);
             k.ns++;
             k.nt += L;
             k.sum_l2 += (double)L * L;

@@ -29,7 +29,8 @@ from typing import Mapping
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# FUTON_ORACLE_LIB selects another build of oracle.c (the sanitizer test's).
+_LIB_PATH = os.environ.get("FUTON_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 
