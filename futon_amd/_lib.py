@@ -26,7 +26,8 @@ FH_OP_ACT_NONE, FH_OP_ACT_GELU, FH_OP_ACT_SWIGLU = 0, 1, 2
 
 # Every symbol the public headers declare (checked by the CPU test suite).
 EXPORTED = (
-    "fh_model_create", "fh_model_destroy", "fh_encode", "fh_encode_device", "fh_profile_enable",
+    "fh_model_create", "fh_model_destroy", "fh_encode", "fh_encode_device", "fh_encode_device_noalloc",
+    "fh_noalloc_scratch_bytes", "fh_profile_enable",
     "fh_profile_reset", "fh_profile_read", "fh_debug_cancel_after", "fh_checkpoints_per_call",
     "fh_strerror", "fh_last_error", "fh_model_device_bytes",
     "fh_op_gemm", "fh_op_gemm_ring", "fh_op_gemm_ln", "fh_op_row_stats", "fh_op_ring_pack", "fh_op_mlp_pack", "fh_op_mlp", "fh_op_outproj_mlp", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
@@ -94,6 +95,10 @@ def load():
     L.fh_encode.argtypes = [vp, vp, vp, i32, i32, vp, vp]
     L.fh_encode_device.restype = ctypes.c_int
     L.fh_encode_device.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]
+    L.fh_encode_device_noalloc.restype = ctypes.c_int
+    L.fh_encode_device_noalloc.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]
+    L.fh_noalloc_scratch_bytes.restype = ctypes.c_int64
+    L.fh_noalloc_scratch_bytes.argtypes = []
     L.fh_profile_enable.argtypes = [vp, i32]
     L.fh_profile_reset.argtypes = [vp]
     L.fh_profile_read.argtypes = [vp, vp, vp, vp, vp, vp, i32]

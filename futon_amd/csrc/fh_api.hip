@@ -28,9 +28,44 @@
 #include "fh_common.h"
 #include "host/host_common.h"
 
+// Device memory of fh_encode_device_noalloc: every buffer of a forward
+// beyond its inputs and outputs (the workspace fh_encode_device allocates),
+// in one array per device, held until the process ends.  Host code never
+// uses the name itself: fh_model_create looks up each device's address
+// (hipGetSymbolAddress) once, and the entry point passes that address on.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 using fh::fail;
+
+// Per device: the scratch array's device address, and the event that marks
+// the end of the last forward that used it (later calls queue behind it,
+// whatever stream or model they come from).
+constexpr int kMaxDevices = 64;
+struct DevScratch {
+    void *ptr = nullptr;
+    hipEvent_t done = nullptr;
+    bool used = false;
+};
+std::mutex g_scratch_mu;
+DevScratch g_scratch[kMaxDevices];
+
+// Once per device, with that device current.
+int init_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(FH_ENODEV, "device %d beyond %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    DevScratch &d = g_scratch[device];
+    if (d.ptr) return FH_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(FH_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+    if (e != hipSuccess) return fail(FH_EHIP, "hipEventCreate: %s", hipGetErrorString(e));
+    d.ptr = p;
+    return FH_OK;
+}
 
 #define HIPCHK(expr)                                                                       \
     do {                                                                                   \
@@ -1065,6 +1100,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     if (!strstr(prop.gcnArchName, "gfx950"))
         return fail(FH_ENODEV, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
     HIPCHK(hipSetDevice(device));
+    if (int rs = init_scratch(device)) return rs;
 
     fh_model *m = new fh_model();
     m->cfg = c;
@@ -1400,6 +1436,61 @@ extern "C" int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t
     const int rc_end = end_on(m, s);
     return rc ? rc : rc_end;
 }
+
+extern "C" int fh_encode_device_noalloc(fh_model *m, const int32_t *d_ids, const int32_t *d_offsets, int32_t nseq,
+                                        int32_t total_tokens, int32_t max_len, int32_t out_dim, float *d_out,
+                                        void *stream, const int32_t *h_offsets) {
+    if (!m) return fail(FH_EINVAL, "native: null model");
+    if (nseq <= 0) return nseq == 0 ? FH_OK : fail(FH_EINVAL, "native: negative batch size");
+    if (!d_ids || !d_offsets || !d_out) return fail(FH_EINVAL, "native: null buffer");
+    const fh_config &c = m->cfg;
+    if (out_dim < 0 || out_dim > c.hidden_size || (out_dim != 0 && out_dim != c.hidden_size && !c.matryoshka))
+        return fail(FH_EINVAL, "native: requested dim %d not supported", out_dim);
+    if (max_len <= 0 || max_len > m->eff_max || total_tokens < nseq || total_tokens > (int64_t)nseq * max_len)
+        return fail(FH_EINVAL, "native: inconsistent batch description (T=%d, nseq=%d, max_len=%d)", total_tokens,
+                    nseq, max_len);
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIPCHK(hipSetDevice(m->device));
+    DevScratch &d = g_scratch[m->device];
+    if (!d.ptr) return fail(FH_EHIP, "scratch of device %d not set up", m->device);
+    const WsPlan plan = workspace_plan(m, total_tokens, nseq);
+    const size_t need = workspace_bytes(plan);
+    if (need > kScratchBytes)
+        return fail(FH_EINVAL,
+                    "native: batch of %d tokens in %d sequences needs %zu bytes of scratch; the no-allocation entry "
+                    "point holds %zu (use fh_encode_device)",
+                    total_tokens, nseq, need, kScratchBytes);
+    BatchInfo b{d_ids, d_offsets, nseq, total_tokens, max_len, out_dim, d_out};
+    if (h_offsets) {
+        for (int i = 0; i < nseq; i++) {
+            const double L = (double)(h_offsets[i + 1] - h_offsets[i]);
+            b.sum_l2 += L * L;
+        }
+    }
+    // The model's buffers point into the scratch for this call only, and the
+    // profiler (which creates events) is off for it.
+    void *saved[20];
+    for (int i = 0; i < plan.n; i++) saved[i] = *plan.e[i].first;
+    const bool prof = m->prof;
+    m->prof = false;
+    carve(plan, (char *)d.ptr);
+    hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+    int rc = FH_OK;
+    {
+        std::lock_guard<std::mutex> sl(g_scratch_mu);
+        hipError_t e = d.used ? hipStreamWaitEvent(s, d.done, 0) : hipSuccess;
+        if (e != hipSuccess) rc = fail(FH_EHIP, "hipStreamWaitEvent: %s", hipGetErrorString(e));
+        if (rc == FH_OK) rc = run_forward(m, b, s);
+        e = hipEventRecord(d.done, s);
+        if (e == hipSuccess) d.used = true;
+        else if (rc == FH_OK) rc = fail(FH_EHIP, "hipEventRecord: %s", hipGetErrorString(e));
+    }
+    for (int i = 0; i < plan.n; i++) *plan.e[i].first = saved[i];
+    m->prof = prof;
+    return rc;
+}
+
+extern "C" int64_t fh_noalloc_scratch_bytes(void) { return (int64_t)kScratchBytes; }
 
 extern "C" int32_t fh_route_flags(int32_t hidden, int32_t inter, int32_t swiglu, int32_t M) {
     if (hidden <= 0 || inter <= 0 || M <= 0) return 0;

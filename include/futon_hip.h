@@ -121,6 +121,23 @@ int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t *d_offsets
                      int32_t total_tokens, int32_t max_len, int32_t out_dim, float *d_out,
                      void *stream, const int32_t *h_offsets);
 
+/* fh_encode_device without any device allocation: the same forward, same
+ * bits, with its workspace in a fixed scratch array that each device holds
+ * from model creation until the process ends (fh_noalloc_scratch_bytes,
+ * 64 MiB: ≈ 6.6k tokens of a hidden-384 pack, ≈ 3.3k of hidden 768).  A
+ * batch whose workspace exceeds it is FH_EINVAL and nothing runs.  Calls no
+ * hipMalloc/hipFree and creates nothing (not profiled).  Every call on a
+ * device shares that device's array: calls are queued behind the previous
+ * call that used it (an event, whatever the stream or model), so they never
+ * overlap on the GPU; a caller must not expect two such calls to run
+ * concurrently.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int fh_encode_device_noalloc(fh_model *m, const int32_t *d_ids, const int32_t *d_offsets, int32_t nseq,
+                             int32_t total_tokens, int32_t max_len, int32_t out_dim, float *d_out,
+                             void *stream, const int32_t *h_offsets);
+int64_t fh_noalloc_scratch_bytes(void);
+
 /* Per-kernel-class timing with HIP events around every launch of
  * fh_encode_device (off by default).  fh_profile_read copies up to `cap`
  * entries: names (static strings), total milliseconds, launch counts, and
