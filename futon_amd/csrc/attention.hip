@@ -78,6 +78,7 @@ void attn_kernel(AttnArgs a) {
             head = t % gy;
             seq = t / gy;
         }
+        seq += a.seq0;
     }
     const int start = a.offsets[seq];
     const int L = a.offsets[seq + 1] - start;

@@ -206,6 +206,7 @@ struct fh_model {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     float *x32 = nullptr, *y32 = nullptr, *xc32 = nullptr;
+    float *pool_part = nullptr;  // mean pooling's segment sums
     f16 *x16 = nullptr, *qkv = nullptr, *xc16 = nullptr;
     void *attn = nullptr, *attnc = nullptr, *hbuf = nullptr;
     int8_t *xq = nullptr;
@@ -219,8 +220,8 @@ struct fh_model {
     void *pin = nullptr;
     size_t pin_bytes = 0;
     int chunk_tokens = 1 << 18;  // most tokens one fh_encode chunk runs in one forward
-    bool schedule = true;        // sort and split fh_encode batches by attention class (FUTON_SCHEDULE=0: one
-                                 // forward in batch order, for comparison)
+    bool schedule = true;        // sort fh_encode batches and split attention by class (FUTON_SCHEDULE=0: batch
+                                 // order, one attention launch sized by the longest sequence; for comparison)
     // Every forward is ordered after the previous one, whatever stream each
     // ran on: done_ev is recorded at the end of each forward (done_stream is
     // where), and the next forward's stream waits on it.  Synchronizing
@@ -500,6 +501,7 @@ WsPlan workspace_plan(fh_model *m, int T, int S) {
         {(void **)&m->sA, (size_t)T * 8},             {(void **)&m->sB, (size_t)T * 8},
         {(void **)&m->sAc, (size_t)S * 8},            {(void **)&m->sBc, (size_t)S * 8},
         {(void **)&m->yBc, (size_t)S * H * 2},
+        {(void **)&m->pool_part, (size_t)fh::pool_part_rows(T, S) * H * 4},
     })
         plan.push_back(p);
     if (q8) {
@@ -630,7 +632,31 @@ struct BatchInfo {
     bool host_checks = false;  // cancellation checkpoints active
     Pacer *pacer = nullptr;    // non-null: pace the enqueue against execution
     int *cp_base = nullptr;    // running checkpoint count across the call's chunks
+    // Sequences sorted longest first, the first n_long longer than one key
+    // block: attention runs as two launches, [0, n_long) on the multi-block
+    // path and [n_long, nseq) (at most max_short tokens) on the one-block
+    // path, so each sequence takes its own class's path whatever else is in
+    // the batch.  n_long = 0: one launch sized by max_len.
+    int n_long = 0, max_short = 0;
 };
+
+// Sets n_long/max_short when host offsets show a longest-first batch that
+// mixes the two attention classes.
+void classify(BatchInfo &b, const int32_t *h_offsets) {
+    if (!h_offsets) return;
+    int n_long = 0, prev = INT_MAX, max_short = 0;
+    for (int i = 0; i < b.nseq; i++) {
+        const int L = h_offsets[i + 1] - h_offsets[i];
+        if (L > prev) return;  // not longest first: one launch
+        prev = L;
+        if (L > fh::ATTN_ONE_BLOCK_KEYS) n_long++;
+        else max_short = std::max(max_short, L);
+    }
+    if (n_long > 0 && n_long < b.nseq) {
+        b.n_long = n_long;
+        b.max_short = max_short;
+    }
+}
 
 #define LCHK(expr)                                                                         \
     do {                                                                                   \
@@ -654,6 +680,17 @@ int checkpoint(fh_model *m, const BatchInfo &b, int &cp, hipStream_t s) {
         return fail(FH_ECANCELED, "native: context canceled at checkpoint %d", idx);
     }
     return FH_OK;
+}
+
+hipError_t attend(AttnArgs a, const BatchInfo &b, bool out_f32, hipStream_t s) {
+    a.seq0 = 0;
+    if (b.n_long > 0 && b.n_long < b.nseq) {
+        const hipError_t e = fh::attention(a, b.n_long, b.max_len, out_f32, s);
+        if (e != hipSuccess) return e;
+        a.seq0 = b.n_long;
+        return fh::attention(a, b.nseq - b.n_long, b.max_short, out_f32, s);
+    }
+    return fh::attention(a, b.nseq, b.max_len, out_f32, s);
 }
 
 int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const float *a_scale, int M,
@@ -875,7 +912,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             const double nq_l = last_cls ? (double)T : b.sum_l2;
             Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * 2,
                      s);
-            LCHK(fh::attention(a, S, b.max_len, false, s));
+            LCHK(attend(a, b, false, s));
         }
 
         const int M = last_cls ? S : T;
@@ -928,8 +965,8 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
     {
         const int od = b.out_dim == 0 ? H : b.out_dim;
         Scope sc(m, K_POOL, 0.0, (cls ? (double)S * H * 4 : (double)T * H * 4) + (double)S * od * 4, s);
-        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, H, cls ? 1 : 0, cls ? 0 : 1, c.matryoshka_layernorm,
-                      od, c.normalize, b.d_out, s));
+        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, b.max_len, H, cls ? 1 : 0, cls ? 0 : 1,
+                      c.matryoshka_layernorm, od, c.normalize, m->pool_part, b.d_out, s));
     }
     return FH_OK;
 }
@@ -987,7 +1024,7 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
             const double nq_l = last_cls ? (double)T : b.sum_l2;  // Σ nq·L
             Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * (q8 ? 4 : 2),
                      s);
-            LCHK(fh::attention(a, S, b.max_len, q8, s));
+            LCHK(attend(a, b, q8, s));
         }
 
         const int M = last_cls ? S : T;
@@ -1044,8 +1081,8 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
     {
         const int od = b.out_dim == 0 ? H : b.out_dim;
         Scope sc(m, K_POOL, 0.0, (cls ? (double)S * H * 4 : (double)T * H * 4) + (double)S * od * 4, s);
-        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, H, cls ? 1 : 0, cls ? 0 : 1,
-                      c.matryoshka_layernorm, od, c.normalize, b.d_out, s));
+        LCHK(fh::pool(cls ? m->xc32 : m->x32, b.d_offsets, S, b.max_len, H, cls ? 1 : 0, cls ? 0 : 1,
+                      c.matryoshka_layernorm, od, c.normalize, m->pool_part, b.d_out, s));
     }
     return FH_OK;
 }
@@ -1305,13 +1342,14 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
     const int od = out_dim == 0 ? c.hidden_size : out_dim;
 
     // Schedule (the batch counterpart of the reference's longest-first
-    // dispatch, provider.go:183-246): sequences sorted longest first, cut
-    // into chunks that each hold one attention class — every sequence fits
-    // one key block (≤ fh::ATTN_ONE_BLOCK_KEYS keys), or none does — and at
-    // most chunk_tokens tokens.  Each chunk is one packed forward, so a long
-    // sequence does not move the short ones onto the multi-block attention
-    // path, and a sequence's vector (computed in a fixed order by kernels
-    // chosen only by its own class) is the same bits in any batch.
+    // dispatch, provider.go:183-246): sequences sorted longest first and cut
+    // into chunks of at most chunk_tokens tokens, each one packed forward.
+    // Inside a chunk the sequences longer than one key block
+    // (fh::ATTN_ONE_BLOCK_KEYS) form a prefix, and attention runs once over
+    // that prefix and once over the rest, so a long sequence does not move
+    // the short ones onto the multi-block path while the GEMMs still see the
+    // whole chunk.  A sequence's vector (fixed reduction orders, kernels
+    // chosen only by its own class) is then the same bits in any batch.
     std::vector<int> ord((size_t)nseq);
     for (int i = 0; i < nseq; i++) ord[(size_t)i] = i;
     auto len = [&](int i) { return seq_offsets[i + 1] - seq_offsets[i]; };
@@ -1319,6 +1357,7 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
     struct Chunk {
         int s0, ns, t0, nt, max_len;
         double sum_l2;
+        int n_long, max_short;  // sequences past one key block (a prefix: longest first), longest of the rest
     };
     std::vector<Chunk> chunks;
     int max_nt = 0, max_ns = 0;
@@ -1327,11 +1366,11 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
         for (int j = 0; j < nseq; j++) {
             const int L = len(ord[(size_t)j]);
             const bool one = L <= fh::ATTN_ONE_BLOCK_KEYS;
-            if (chunks.empty() || chunks.back().nt + L > m->chunk_tokens ||
-                (m->schedule && (chunks.back().max_len <= fh::ATTN_ONE_BLOCK_KEYS) != one))
-                chunks.push_back({j, 0, t, 0, L, 0.0});
+            if (chunks.empty() || chunks.back().nt + L > m->chunk_tokens) chunks.push_back({j, 0, t, 0, L, 0.0, 0, 0});
             Chunk &k = chunks.back();
             k.max_len = std::max(k.max_len, L);
+            if (m->schedule && !one) k.n_long++;
+            if (one) k.max_short = std::max(k.max_short, L);
             k.ns++;
             k.nt += L;
             k.sum_l2 += (double)L * L;
@@ -1382,6 +1421,10 @@ extern "C" int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_off
         BatchInfo b{(const int32_t *)(io + off_ids) + k.t0, (const int32_t *)(io + off_offs) + k.s0 + ci, k.ns, k.nt,
                     k.max_len, out_dim, (float *)(io + off_out) + (size_t)k.s0 * od};
         b.sum_l2 = k.sum_l2;
+        if (k.n_long > 0 && k.n_long < k.ns) {
+            b.n_long = k.n_long;
+            b.max_short = k.max_short;
+        }
         b.cancel = cancel;
         b.host_checks = true;
         b.pacer = pace ? &pacer : nullptr;
@@ -1430,6 +1473,7 @@ extern "C" int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t
     } else {
         b.sum_l2 = (double)total_tokens * max_len;  // upper bound without host offsets
     }
+    classify(b, h_offsets);
     hipStream_t s = stream ? (hipStream_t)stream : m->stream;
     if ((rc = begin_on(m, s))) return rc;
     rc = run_forward(m, b, s);
@@ -1467,6 +1511,7 @@ extern "C" int fh_encode_device_noalloc(fh_model *m, const int32_t *d_ids, const
             b.sum_l2 += L * L;
         }
     }
+    classify(b, h_offsets);
     // The model's buffers point into the scratch for this call only, and the
     // profiler (which creates events) is off for it.
     void *saved[20];

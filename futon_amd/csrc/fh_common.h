@@ -84,6 +84,7 @@ struct AttnArgs {
     const float *rope_sin;
     void *out;             // [T or nseq, ldo]
     int H, d, ldo;
+    int seq0;              // first sequence of this launch (blockIdx.z counts from it)
     int q_limit;           // queries per sequence that produce output (1 = CLS row)
     int compact;           // output row = sequence index (CLS mode)
     float scale_log2e;     // (1/sqrt(d)) * log2(e)
@@ -189,6 +190,14 @@ hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const 
                        float *xc32, f16 *xc16, f32x2 *stc, hipStream_t s);
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
                          hipStream_t s);
-hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact,
-                int mean, int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s);
+// Mean pooling sums each sequence in POOL_SEG-token segments (token order
+// inside a segment), then the segments in order.  `part` holds the segment
+// sums: pool_part_rows(T, nseq) rows of H floats; sequence q's segments
+// start at row pool_part_row(offsets[q], q) (≥ the previous sequence's
+// last segment + 1, since ⌊a/G⌋ + ⌈L/G⌉ ≤ ⌊(a+L)/G⌋ + 1).
+constexpr int POOL_SEG = 64;
+__host__ __device__ inline int64_t pool_part_row(int64_t start, int64_t seq) { return start / POOL_SEG + seq; }
+inline int64_t pool_part_rows(int64_t T, int64_t nseq) { return T / POOL_SEG + nseq + 1; }
+hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int max_len, int H, int cls_compact,
+                int mean, int matryoshka_ln, int out_dim, int normalize, float *part, float *out, hipStream_t s);
 }  // namespace fh

@@ -2,7 +2,9 @@
 // then the same launchers fh_encode uses.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
+#include <vector>
 #include <cmath>
 
 #include "../../include/futon_hip.h"
@@ -229,7 +231,26 @@ extern "C" int fh_op_embed_ln(const int32_t *ids, const int32_t *offsets, int32_
 
 extern "C" int fh_op_pool(const float *x32, const int32_t *offsets, int32_t nseq, int32_t H, int32_t cls_compact,
                           int32_t matryoshka_ln, int32_t out_dim, int32_t normalize, float *out, void *stream) {
-    if (!x32 || !offsets || !out || H <= 0 || H > 1024 || out_dim <= 0 || out_dim > H) return FH_EINVAL;
-    return code_of(fh::pool(x32, offsets, nseq, H, cls_compact, cls_compact ? 0 : 1, matryoshka_ln, out_dim,
-                            normalize, out, (hipStream_t)stream));
+    if (!x32 || !offsets || !out || H <= 0 || H > 1024 || H % 4 || out_dim <= 0 || out_dim > H || nseq < 0)
+        return FH_EINVAL;
+    if (nseq == 0) return FH_OK;
+    // Mean pooling needs its segment-sum buffer: sized from the offsets (a
+    // test entry point, so it reads them back and allocates here).
+    std::vector<int32_t> h((size_t)nseq + 1);
+    hipStream_t s = (hipStream_t)stream;
+    if (hipMemcpyAsync(h.data(), offsets, h.size() * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return FH_EHIP;
+    int max_len = 0;
+    for (int i = 0; i < nseq; i++) max_len = std::max(max_len, h[(size_t)i + 1] - h[(size_t)i]);
+    float *part = nullptr;
+    if (!cls_compact && hipMalloc(&part, (size_t)fh::pool_part_rows(h[(size_t)nseq], nseq) * H * 4) != hipSuccess)
+        return FH_ENOMEM;
+    const hipError_t e = fh::pool(x32, offsets, nseq, std::max(max_len, 1), H, cls_compact, cls_compact ? 0 : 1,
+                                  matryoshka_ln, out_dim, normalize, part, out, s);
+    if (part) {
+        hipStreamSynchronize(s);
+        hipFree(part);
+    }
+    return code_of(e);
 }

@@ -311,11 +311,40 @@ __device__ double block_sum_f64(double v, double *red) {
     return t;
 }
 
+// Mean pooling, first stage: the float32 column sums of each POOL_SEG-token
+// segment of each sequence, in token order, over the whole chip (one block
+// per (segment, sequence), 4 columns per thread).  Segment j of sequence q
+// goes to partial row fh::pool_part_row(offsets[q], q) + j: the rows of
+// different sequences never overlap, and a sequence's sums do not depend
+// on the rest of the batch.
+__global__ __launch_bounds__(256) void pool_partial_kernel(const float *__restrict__ x32,
+                                                           const int32_t *__restrict__ offsets, int H,
+                                                           float *__restrict__ part) {
+    const int seq = blockIdx.y, j = blockIdx.x;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    const int t0 = j * fh::POOL_SEG;
+    if (t0 >= L) return;
+    const int t1 = min(L, t0 + fh::POOL_SEG);
+    float *dst = part + (size_t)(fh::pool_part_row(start, seq) + j) * H;
+    for (int c = threadIdx.x * 4; c < H; c += blockDim.x * 4) {
+        const float *src = x32 + (size_t)(start + t0) * H + c;
+        f32x4 acc = *(const f32x4 *)src;
+        for (int t = t0 + 1; t < t1; ++t) {
+            src += H;
+            const f32x4 v = *(const f32x4 *)src;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], v[i]);
+        }
+        *(f32x4 *)(dst + c) = acc;
+    }
+}
+
 // Pool → Matryoshka → L2 — native/model.go:417-453.  One block per sequence.
-// CLS reads row seq of the compact last-layer buffer; mean sums the
-// sequence's rows in token order in float32 and scales by float32(1/L).
-__global__ __launch_bounds__(256) void pool_kernel(const float *x32, const int32_t *offsets, int H,
-                                                   int cls_compact, int mean, int mat_ln, int out_dim,
+// CLS reads row seq of the compact last-layer buffer; mean adds the
+// sequence's segment sums (pool_partial_kernel) in segment order in float32
+// and scales by float32(1/L).
+__global__ __launch_bounds__(256) void pool_kernel(const float *x32, const float *part, const int32_t *offsets,
+                                                   int H, int cls_compact, int mean, int mat_ln, int out_dim,
                                                    int normalize, float *out) {
     __shared__ float pooled[1024];
     __shared__ double red[4];
@@ -324,9 +353,10 @@ __global__ __launch_bounds__(256) void pool_kernel(const float *x32, const int32
     for (int e = threadIdx.x; e < H; e += blockDim.x) {
         float p;
         if (mean) {
-            p = 0.f;
-            const float *col = x32 + (size_t)start * H + e;
-            for (int t = 0; t < L; ++t) p = __fadd_rn(p, col[(size_t)t * H]);
+            const int nseg = (L + fh::POOL_SEG - 1) / fh::POOL_SEG;
+            const float *col = part + (size_t)fh::pool_part_row(start, seq) * H + e;
+            p = col[0];
+            for (int j = 1; j < nseg; ++j) p = __fadd_rn(p, col[(size_t)j * H]);
             p = __fmul_rn(p, __fdiv_rn(1.0f, (float)L));
         } else {
             p = x32[(size_t)(cls_compact ? seq : start) * H + e];
@@ -436,10 +466,15 @@ hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float
     hipLaunchKernelGGL(quantize_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, M, K, ldx, q, scale);
     return hipGetLastError();
 }
-hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int H, int cls_compact, int mean,
-                int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s) {
+hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int max_len, int H, int cls_compact, int mean,
+                int matryoshka_ln, int out_dim, int normalize, float *part, float *out, hipStream_t s) {
     if (nseq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pool_kernel, dim3(nseq), dim3(256), 0, s, x32, offsets, H, cls_compact, mean,
+    if (mean) {
+        if (!part || H % 4 || max_len <= 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(pool_partial_kernel, dim3((max_len + POOL_SEG - 1) / POOL_SEG, nseq), dim3(256), 0, s, x32,
+                           offsets, H, part);
+    }
+    hipLaunchKernelGGL(pool_kernel, dim3(nseq), dim3(256), 0, s, x32, part, offsets, H, cls_compact, mean,
                        matryoshka_ln, out_dim, normalize, out);
     return hipGetLastError();
 }

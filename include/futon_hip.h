@@ -114,8 +114,13 @@ int fh_encode(fh_model *m, const int32_t *ids, const int32_t *seq_offsets, int32
  * them while the ids live on the device).  Enqueued on `stream` (a
  * hipStream_t; NULL = the model's own stream) and NOT synchronized.  The
  * caller guarantees the ids were validated.  h_offsets (nullable) is a host
- * copy of d_offsets used only for the profiler's FLOP accounting.  For
- * throughput harnesses whose inputs already reside in HBM.
+ * copy of d_offsets, for the profiler's FLOP accounting and the attention
+ * split: when it shows a longest-first batch that mixes sequences of at most
+ * 128 tokens with longer ones, each class runs its own attention path, so
+ * every vector equals its single-sequence forward (as fh_encode, which sorts
+ * the batch itself, always does); otherwise one attention launch sized by
+ * max_len serves the whole batch.  For throughput harnesses whose inputs
+ * already reside in HBM.
  * Replaces: the same as fh_encode. */
 int fh_encode_device(fh_model *m, const int32_t *d_ids, const int32_t *d_offsets, int32_t nseq,
                      int32_t total_tokens, int32_t max_len, int32_t out_dim, float *d_out,
