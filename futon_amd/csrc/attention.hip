@@ -17,6 +17,7 @@
 // from registers (the key order inside the contraction is permuted
 // identically on both operands).  Q fragments are loaded from global memory
 // directly in the MFMA operand layout.
+#include <cstdlib>
 #include <type_traits>
 
 #include "fh_common.h"
@@ -29,6 +30,20 @@ namespace {
 #ifndef ATTN_ONE_WAVES
 #define ATTN_ONE_WAVES 6
 #endif
+#ifndef ATTN_LONG_WAVES
+#define ATTN_LONG_WAVES 4
+#endif
+#ifndef ATTN_LONG_QT
+#define ATTN_LONG_QT 2
+#endif
+
+// Sequences past one key block take the pipelined kernel (attn_long_kernel)
+// unless FUTON_ATTN_LONG=0 (read per launch; diagnostics and the
+// bit-equality test against attn_kernel's multi-block path).
+bool long_pipeline() {
+    const char *e = getenv("FUTON_ATTN_LONG");
+    return !(e && e[0] == '0');
+}
 
 // With one key block and 32-wide heads the kernel fits in 80 VGPRs without
 // spills: ask for six waves per SIMD (four at the compiler's own choice of
@@ -37,67 +52,54 @@ namespace {
 template <int D, int WAVES, bool ONE>
 constexpr int attn_min_waves() { return (ONE && D == 32 && WAVES >= 4) ? ATTN_ONE_WAVES : 1; }
 
-template <int D, int WAVES, int QT, int KBLK, bool OUT_F32, bool ROPE, bool ONE>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(attn_min_waves<D, WAVES, ONE>(), 8)))
-void attn_kernel(AttnArgs a) {
-    // ONE: every sequence fits in one key block (L <= KBLK), so each query
-    // tile is finished (softmax, PV, normalise, store) before the next one
-    // starts and only one tile's output and statistics are live at a time.
-    // The arithmetic is the same as the multi-block path's first block
-    // (running max -inf, running sum 0), so the results are the same bits.
-    constexpr int QROWS = 16 * QT * WAVES;
-    constexpr int QS = ONE ? 1 : QT;  // query tiles with live softmax state
-    constexpr int KS = D + 8;     // K LDS row stride (halves)
-    constexpr int VS = KBLK + 8;  // Vᵀ LDS row stride (halves)
-    constexpr int NKT = KBLK / 16;
-    static_assert(KBLK % 32 == 0, "PV consumes 32-key chunks");
-    __shared__ __attribute__((aligned(16))) f16 Ks[KBLK * KS];
-    __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
-
-    // Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
-    // contiguous range of items, ordered so that blocks which read the same
-    // qkv lines share one L2 (the lines are then fetched once, not once per
-    // XCD).
-    int seq, head, qg;
-    {
-        const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * gridDim.z;
-        const int pid = (blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
-        const int xcd = pid & 7, idx = pid >> 3, q8 = nb >> 3, r8 = nb & 7;
-        const int logical = xcd * q8 + min(xcd, r8) + idx;
-        qg = logical % gx;
-        const int t = logical / gx;
-        if (ATTN_PAIR_ORDER && (gy & 1) == 0) {
-            // (head pair, sequence, head) order: the two heads whose q/k/v
-            // segments share 128-byte lines stay on one XCD, and each XCD's
-            // range spans many sequences, so per-XCD work varies less than
-            // with whole sequences per XCD.
-            const int nseq = gridDim.z, u = t >> 1;
-            head = (u / nseq) * 2 + (t & 1);
-            seq = u % nseq;
-        } else {
-            head = t % gy;
-            seq = t / gy;
-        }
-        seq += a.seq0;
+// Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
+// contiguous range of (query group, head, sequence) items, ordered so that
+// blocks which read the same qkv lines share one L2 (the lines are then
+// fetched once, not once per XCD).
+__device__ __forceinline__ void block_item(const AttnArgs &a, int &seq, int &head, int &qg) {
+    const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy * gridDim.z;
+    const int pid = (blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
+    const int xcd = pid & 7, idx = pid >> 3, q8 = nb >> 3, r8 = nb & 7;
+    const int logical = xcd * q8 + min(xcd, r8) + idx;
+    qg = logical % gx;
+    const int t = logical / gx;
+    if (ATTN_PAIR_ORDER && (gy & 1) == 0) {
+        // (head pair, sequence, head) order: the two heads whose q/k/v
+        // segments share 128-byte lines stay on one XCD, and each XCD's
+        // range spans many sequences, so per-XCD work varies less than with
+        // whole sequences per XCD.
+        const int nseq = gridDim.z, u = t >> 1;
+        head = (u / nseq) * 2 + (t & 1);
+        seq = u % nseq;
+    } else {
+        head = t % gy;
+        seq = t / gy;
     }
-    const int start = a.offsets[seq];
-    const int L = a.offsets[seq + 1] - start;
-    const int nq = min(L, a.q_limit);
-    const int q0 = qg * QROWS;
-    if (q0 >= nq) return;
+    seq += a.seq0;
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int d = a.d, H = a.H, ld = 3 * H;
-    const int half = d >> 1;
-    const int chunks = d >> 3;  // 16-byte chunks per row (d % 8 == 0)
+// rotateHalf's two products and their difference (first half) or sum
+// (second half), each rounded to float32 on its own as the reference's Go
+// code computes them, the same in every kernel: contraction into a fused
+// multiply-add is switched off here (hipcc contracts by default, and the
+// __f*_rn helpers are plain operators in this toolchain).
+__device__ __forceinline__ float rot(float x, float partner, float cs, float sn, bool first) {
+#pragma clang fp contract(off)
+    const float a = x * cs, b = partner * sn;
+    return first ? a - b : a + b;
+}
+
+// Q fragments of QT 16-query tiles (B operand of Sᵀ = K·Qᵀ): lane holds
+// dims [dk·32 + (lane/16)·8, +8) of query lane%16 of each tile, rotated
+// (rotateHalf, model.go:705-712) when the pack uses RoPE.
+template <int D, int QT, bool ROPE>
+__device__ __forceinline__ void load_q(const AttnArgs &a, int start, int L, int qbase, int lane,
+                                       f16x8 (&qf)[QT][D / 32], int head) {
+    const int d = a.d, half = d >> 1, ld = 3 * a.H;
     const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
-
-    // ── Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds dims
-    //    [dk·32 + (lane/16)·8, +8) of query lane%16 of each tile. ──
-    f16x8 qf[QT][D / 32];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const int q = min(q0 + (wave * QT + qt) * 16 + (lane & 15), L - 1);
+        const int q = min(qbase + qt * 16 + (lane & 15), L - 1);
         const f16 *qrow = a.qkv + (size_t)(start + q) * ld + head * d;
 #pragma unroll
         for (int dk = 0; dk < D / 32; ++dk) {
@@ -119,13 +121,48 @@ void attn_kernel(AttnArgs a) {
                     if (half >= 8) partner = (float)p[e];
                     else partner = (float)v[(e + half) & 7];
                     const float x = (float)v[e];
-                    r[e] = (f16)(j < half ? x * cs - partner * sn : x * cs + partner * sn);
+                    r[e] = (f16)rot(x, partner, cs, sn, j < half);
                 }
                 v = r;
             }
             qf[qt][dk] = v;
         }
     }
+}
+
+template <int D, int WAVES, int QT, int KBLK, bool OUT_F32, bool ROPE, bool ONE>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(attn_min_waves<D, WAVES, ONE>(), 8)))
+void attn_kernel(AttnArgs a) {
+    // ONE: every sequence fits in one key block (L <= KBLK), so each query
+    // tile is finished (softmax, PV, normalise, store) before the next one
+    // starts and only one tile's output and statistics are live at a time.
+    // The arithmetic is the same as the multi-block path's first block
+    // (running max -inf, running sum 0), so the results are the same bits.
+    constexpr int QROWS = 16 * QT * WAVES;
+    constexpr int QS = ONE ? 1 : QT;  // query tiles with live softmax state
+    constexpr int KS = D + 8;     // K LDS row stride (halves)
+    constexpr int VS = KBLK + 8;  // Vᵀ LDS row stride (halves)
+    constexpr int NKT = KBLK / 16;
+    static_assert(KBLK % 32 == 0, "PV consumes 32-key chunks");
+    __shared__ __attribute__((aligned(16))) f16 Ks[KBLK * KS];
+    __shared__ __attribute__((aligned(16))) f16 Vt[D * VS];
+
+    int seq, head, qg;
+    block_item(a, seq, head, qg);
+    const int start = a.offsets[seq];
+    const int L = a.offsets[seq + 1] - start;
+    const int nq = min(L, a.q_limit);
+    const int q0 = qg * QROWS;
+    if (q0 >= nq) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int d = a.d, H = a.H, ld = 3 * H;
+    const int half = d >> 1;
+    const int chunks = d >> 3;  // 16-byte chunks per row (d % 8 == 0)
+    const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+
+    f16x8 qf[QT][D / 32];
+    load_q<D, QT, ROPE>(a, start, L, q0 + wave * QT * 16, lane, qf, head);
 
     f32x4 o[QS][D / 16];
     float m_run[QS], l_run[QS];
@@ -218,8 +255,8 @@ void attn_kernel(AttnArgs a) {
                 const int pos = min(kb0 + r, L - 1);
                 const float cs = a.rope_cos[pos * half + i], sn = a.rope_sin[pos * half + i];
                 const float x1 = (float)Ks[r * KS + i], x2 = (float)Ks[r * KS + i + half];
-                Ks[r * KS + i] = (f16)(x1 * cs - x2 * sn);
-                Ks[r * KS + i + half] = (f16)(x2 * cs + x1 * sn);
+                Ks[r * KS + i] = (f16)rot(x1, x2, cs, sn, true);
+                Ks[r * KS + i + half] = (f16)rot(x2, x1, cs, sn, false);
             }
             __syncthreads();
         }
@@ -310,6 +347,226 @@ void attn_kernel(AttnArgs a) {
     }
 }
 
+// Sequences longer than one key block, head width exactly D: the same
+// per-query arithmetic as attn_kernel's multi-block path (Sᵀ = K·Qᵀ per
+// 16-key tile, one online-softmax update per 64-key block, Oᵀ += Vᵀ·Pᵀ over
+// 32-key chunks, keys past the sequence masked to −∞), so both give the same
+// bits, with the key blocks pipelined: the next block's K and V are fetched
+// into registers while the current one is multiplied, rotated (RoPE) and
+// transposed in registers, and written to the other half of a
+// double-buffered LDS stage — one barrier per key block.  Each wave owns QT
+// query tiles, so a block stages each key block once for 16·QT·WAVES
+// queries.
+template <int D, int WAVES, int QT, bool OUT_F32, bool ROPE>
+__global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
+    constexpr int BK = 64, NKT = BK / 16, NC = BK / 32;
+    constexpr int NT = WAVES * 64, QROWS = 16 * QT * WAVES;
+    constexpr int KS = D + 8, VS = BK + 8;  // LDS row pitches (halves)
+    constexpr int CPR = D / 8, HCH = CPR / 2;  // 16-byte chunks per row; RoPE partner distance in chunks
+    // K items: (key, chunk), or with RoPE (key, chunk pair c / c + HCH);
+    // V items: (key pair, chunk), written as Vᵀ key pairs.
+    constexpr int KI = ROPE ? BK * HCH : BK * CPR, VI = BK / 2 * CPR;
+    constexpr int NKI = (KI + NT - 1) / NT, NVI = (VI + NT - 1) / NT;
+    __shared__ __attribute__((aligned(16))) f16 Ks[2][BK * KS];
+    __shared__ __attribute__((aligned(16))) f16 Vt[2][D * VS];
+
+    int seq, head, qg;
+    block_item(a, seq, head, qg);
+    const int start = a.offsets[seq];
+    const int L = a.offsets[seq + 1] - start;
+    const int nq = min(L, a.q_limit);
+    const int q0 = qg * QROWS;
+    if (q0 >= nq) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int H = a.H, ld = 3 * H;
+    const f16 *kbase = a.qkv + (size_t)start * ld + H + head * D, *vbase = kbase + H;
+
+    f16x8 qf[QT][D / 32];
+    load_q<D, QT, ROPE>(a, start, L, q0 + wave * QT * 16, lane, qf, head);
+
+    // Staging registers of one key block.
+    f16x8 rk[NKI][ROPE ? 2 : 1], rv[NVI][2];
+    auto load_kv = [&](int kb0) {
+#pragma unroll
+        for (int i = 0; i < NKI; ++i) {
+            const int c = i * NT + tid;
+            if (KI % NT == 0 || c < KI) {
+                constexpr int PR = ROPE ? HCH : CPR;
+                const int key = min(kb0 + c / PR, L - 1), ch = c % PR;
+                const f16 *r = kbase + (size_t)key * ld + ch * 8;
+                rk[i][0] = *(const f16x8 *)r;
+                if constexpr (ROPE) rk[i][1] = *(const f16x8 *)(r + D / 2);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NVI; ++i) {
+            const int c = i * NT + tid;
+            if (VI % NT == 0 || c < VI) {
+                const int p = c / CPR, ch = c % CPR;
+                rv[i][0] = *(const f16x8 *)(vbase + (size_t)min(kb0 + 2 * p, L - 1) * ld + ch * 8);
+                rv[i][1] = *(const f16x8 *)(vbase + (size_t)min(kb0 + 2 * p + 1, L - 1) * ld + ch * 8);
+            }
+        }
+    };
+    auto store_kv = [&](int buf, int kb0) {
+#pragma unroll
+        for (int i = 0; i < NKI; ++i) {
+            const int c = i * NT + tid;
+            if (KI % NT == 0 || c < KI) {
+                constexpr int PR = ROPE ? HCH : CPR;
+                const int r = c / PR, ch = c % PR;
+                if constexpr (ROPE) {
+                    // rotateHalf on dims i = 8·ch + e and i + D/2 (model.go:705-712)
+                    const int pos = min(kb0 + r, L - 1);
+                    const float *cp = a.rope_cos + (size_t)pos * (D / 2) + ch * 8;
+                    const float *sp = a.rope_sin + (size_t)pos * (D / 2) + ch * 8;
+                    const f32x4 c0 = *(const f32x4 *)cp, c1 = *(const f32x4 *)(cp + 4);
+                    const f32x4 s0 = *(const f32x4 *)sp, s1 = *(const f32x4 *)(sp + 4);
+                    f16x8 lo, hi;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float cs = e < 4 ? c0[e] : c1[e - 4], sn = e < 4 ? s0[e] : s1[e - 4];
+                        const float x1 = (float)rk[i][0][e], x2 = (float)rk[i][1][e];
+                        lo[e] = (f16)rot(x1, x2, cs, sn, true);
+                        hi[e] = (f16)rot(x2, x1, cs, sn, false);
+                    }
+                    *(f16x8 *)&Ks[buf][r * KS + ch * 8] = lo;
+                    *(f16x8 *)&Ks[buf][r * KS + ch * 8 + D / 2] = hi;
+                } else {
+                    *(f16x8 *)&Ks[buf][r * KS + ch * 8] = rk[i][0];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NVI; ++i) {
+            const int c = i * NT + tid;
+            if (VI % NT == 0 || c < VI) {
+                const int p = c / CPR, ch = c % CPR;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    *(f16x2 *)&Vt[buf][(ch * 8 + j) * VS + 2 * p] = (f16x2){rv[i][0][j], rv[i][1][j]};
+            }
+        }
+    };
+
+    f32x4 o[QT][D / 16];
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m_run[qt] = -INFINITY;
+        l_run[qt] = 0.f;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) o[qt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    const float sl2 = a.scale_log2e;
+
+    // One query tile against key block `buf` (kvalid valid keys from its
+    // first).
+    auto qtile = [&](int qt, int buf, int kvalid) {
+        f32x4 s[NKT];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            s[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dk = 0; dk < D / 32; ++dk) {
+                const f16x8 kf = *(const f16x8 *)&Ks[buf][(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qt][dk], s[kt], 0, 0, 0);
+            }
+            if (kvalid < BK) {  // the last key block: keys past the sequence
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (kt * 16 + (lane >> 4) * 4 + i >= kvalid) s[kt][i] = -INFINITY;
+            }
+            mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
+        const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+        float psum = 0.f;
+        f16x8 pf[NC];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = __builtin_amdgcn_exp2f(s[kt][i] * sl2 - m_new);
+                psum += p;
+                pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run[qt] = l_run[qt] * corr + psum;
+        m_run[qt] = m_new;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) o[qt][t] *= corr;
+        // Oᵀ += Vᵀ·Pᵀ over 32-key chunks; key slots {4g..4g+3, 16+4g..16+4g+3}, g = lane/16.
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) {
+                const f16 *vrow = &Vt[buf][(t * 16 + (lane & 15)) * VS + c * 32 + (lane >> 4) * 4];
+                const f16x4 lo = *(const f16x4 *)vrow;
+                const f16x4 hi = *(const f16x4 *)(vrow + 16);
+                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[qt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[qt][t], 0, 0, 0);
+            }
+        }
+    };
+
+    const int nkb = (L + BK - 1) / BK;
+    load_kv(0);
+    store_kv(0, 0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int kb0 = kb * BK, buf = kb & 1;
+        const bool more = kb + 1 < nkb;
+        if (more) load_kv(kb0 + BK);  // in flight while this block is multiplied
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+            if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, L - kb0);  // wave-uniform
+        // The other buffer was last read before the previous barrier.
+        if (more) store_kv(buf ^ 1, kb0 + BK);
+        __syncthreads();
+    }
+
+    // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4] of each tile.
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int q = q0 + (wave * QT + qt) * 16 + (lane & 15);
+        if (q >= nq) continue;
+        const float inv = 1.0f / l_run[qt];
+        const size_t orow = a.compact ? (size_t)seq : (size_t)(start + q);
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+            const int dim = t * 16 + (lane >> 4) * 4;
+            const f32x4 v = o[qt][t] * inv;
+            if (OUT_F32) {
+                *(f32x4 *)((float *)a.out + orow * a.ldo + head * D + dim) = v;
+            } else {
+                const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                *(f16x4 *)((f16 *)a.out + orow * a.ldo + head * D + dim) = h;
+            }
+        }
+    }
+}
+
+template <int D, int WAVES, int QT>
+hipError_t launch_long(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
+    constexpr int QROWS = 16 * QT * WAVES;
+    const int qmax = min(max_len, a.q_limit);
+    dim3 grid((qmax + QROWS - 1) / QROWS, a.H / a.d, nseq);
+    dim3 block(WAVES * 64);
+    if (out_f32) {
+        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, false>), grid, block, 0, s, a);
+    } else {
+        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, false>), grid, block, 0, s, a);
+    }
+    return hipGetLastError();
+}
+
 template <int D, int WAVES, int QT, int KBLK, bool ONE>
 hipError_t launch_d(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
     constexpr int QROWS = 16 * QT * WAVES;
@@ -342,6 +599,7 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
     if (max_len <= 64) return launch_d<D, 2, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
     // Up to 128 tokens: one block covers every query and stages K/V once.
     if (max_len <= fh::ATTN_ONE_BLOCK_KEYS) return launch_d<D, 4, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
+    if (a.d == D && long_pipeline()) return launch_long<D, ATTN_LONG_WAVES, ATTN_LONG_QT>(a, nseq, max_len, out_f32, rope, s);
     return launch_d<D, 4, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
 }
 

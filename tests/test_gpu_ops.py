@@ -546,6 +546,46 @@ def test_attention_matches_float64(H, heads, lens, rope):
     np.testing.assert_allclose(outc.cpu().numpy(), ref[offsets[:-1]], atol=3e-3, rtol=3e-3)
 
 
+@pytest.mark.parametrize("H,heads,lens,rope", [
+    (384, 12, [300, 5, 129, 64, 1000], False),
+    (384, 12, [130, 257], True),
+    (768, 12, [512, 77, 512], False),
+    (768, 12, [2048, 300, 700, 129], True),
+    (1536, 12, [200, 129, 64], True),
+])
+@pytest.mark.parametrize("out_f32", [0, 1])
+def test_long_attention_pipeline_equals_multiblock(H, heads, lens, rope, out_f32, monkeypatch):
+    """Sequences past one key block run on the pipelined kernel
+    (double-buffered K/V, RoPE and the Vᵀ transpose in registers); it keeps
+    the multi-block kernel's per-query arithmetic, so the two return the
+    same bits (FUTON_ATTN_LONG=0 selects the multi-block kernel), and both
+    stay within the float64 tolerance."""
+    rng = np.random.default_rng(H + sum(lens) + out_f32)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(offsets[-1])
+    qkv = (rng.standard_normal((T, 3 * H)) * 1.5).astype(np.float16)
+    d = H // heads
+    tabs = rope_tables(max(lens), d, 1000.0) if rope else None
+    dq, doff = dev(qkv), dev(offsets)
+    dc, ds = (dev(tabs[0]), dev(tabs[1])) if rope else (None, None)
+    outs = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("FUTON_ATTN_LONG", env)
+        out = torch.full((T, H), float("nan"), dtype=torch.float32 if out_f32 else torch.float16, device="cuda")
+        rc = _lib().fh_op_attention(ptr(dq), ptr(doff), len(lens), max(lens), H, heads, ptr(dc), ptr(ds),
+                                    ptr(out), 0, 0, out_f32, None)
+        assert rc == 0
+        sync()
+        outs.append(out.cpu().numpy())
+    a, b = outs
+    assert np.array_equal(a.view(np.uint32 if out_f32 else np.uint16), b.view(np.uint32 if out_f32 else np.uint16))
+    ref = attention_ref(qkv, offsets, heads, tabs)
+    # binary16 probabilities summed over up to 2048 keys (scores of std ≈ 2
+    # here): a looser bound at that length than the 3e-3 of shorter ones.
+    tol = 6e-3 if max(lens) > 1024 else 3e-3
+    np.testing.assert_allclose(a.astype(np.float32), ref, atol=tol, rtol=tol)
+
+
 @pytest.mark.parametrize("y_f16", [0, 1])
 @pytest.mark.parametrize("M,H", [(1, 32), (9, 384), (100, 768), (3, 1024), (5, 256), (7, 160)])
 def test_layer_norm_matches_oracle(M, H, y_f16):
