@@ -851,11 +851,15 @@ int quant(fh_model *m, const float *x, int M, int K, int ldx, hipStream_t s, int
     return FH_OK;
 }
 
+// codes: also write the normalized rows' int8 codes and scales to xq/xs
+// (the next int8 GEMM's activation quantization, fused).
 int layer_norm(fh_model *m, int cls, const float *y32, const f16 *y16, int M, const float *gw, const float *gb,
-               float *x32, f16 *x16, hipStream_t s) {
+               float *x32, f16 *x16, hipStream_t s, bool codes = false) {
     const int H = m->cfg.hidden_size;
-    Scope sc(m, cls, 0.0, (double)M * H * ((y16 ? 2 : 4) + (x32 ? 4 : 0) + 2), s);
-    LCHK(fh::layer_norm(y32, y16, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s));
+    Scope sc(m, cls, 0.0, (double)M * H * ((y16 ? 2 : 4) + (x32 ? 4 : 0) + 2 + (codes ? 1 : 0)) + (codes ? M * 4.0 : 0.0),
+             s);
+    LCHK(fh::layer_norm(y32, y16, M, H, gw, gb, (float)m->cfg.layer_norm_eps, x32, x16, s, codes ? m->xq : nullptr,
+                        codes ? m->xs : nullptr));
     return FH_OK;
 }
 
@@ -987,18 +991,21 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
     int cp = 0, rc;
 
     {
-        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + (f32res ? 6 : 2)) + T * 4.0, s);
+        Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + (f32res ? 6 : 2) + (q8 ? 1 : 0)) + T * 4.0,
+                 s);
+        // Q8: with the first layer's activation codes
         LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, m->emb_w, m->emb_b,
-                          eps, H, f32res ? m->x32 : nullptr, m->x16, s));
+                          eps, H, f32res ? m->x32 : nullptr, m->x16, s, q8 ? m->xq : nullptr, q8 ? m->xs : nullptr,
+                          T));
     }
     for (int li = 0; li < c.num_layers; li++) {
         const DevLayer &L = m->layers[(size_t)li];
         if ((rc = checkpoint(m, b, cp, s))) return rc;
         const bool last = li == c.num_layers - 1, last_cls = cls && last;
 
-        // qkv = x·Wqkvᵀ + b  (model.go:555)
+        // qkv = x·Wqkvᵀ + b  (model.go:555); Q8: x's codes come from the
+        // LayerNorm that produced x (the embedding LN or the previous norm2)
         if (q8) {
-            if ((rc = quant(m, m->x32, T, H, H, s))) return rc;
             rc = gemm(m, K_GEMM_QKV, L.qkv, m->xq, H, m->xs, T, L.qkv_b, nullptr, nullptr, 0, m->qkv, 3 * H,
                       fh::ACT_NONE, false, s);
         } else {
@@ -1052,14 +1059,15 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
                       false, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n1w, L.n1b, f32res ? xo32 : nullptr, xo16, s))) return rc;
+        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n1w, L.n1b,
+                             f32res ? xo32 : nullptr, xo16, s, q8)))
+            return rc;
 
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 
         // FFN (model.go:607-633)
         const int act = swiglu ? fh::ACT_SWIGLU : fh::ACT_GELU;
-        if (q8) {
-            if ((rc = quant(m, xo32, M, H, H, s, kQuant))) return rc;
+        if (q8) {  // x1's codes from norm1 above
             if ((rc = gemm(m, kFfn1, L.ffn1, m->xq, H, m->xs, M, L.ffn1_b, nullptr, nullptr, 0, m->hbuf, I,
                            act, true, s)))
                 return rc;
@@ -1074,7 +1082,10 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
                       false, s);
         }
         if (rc) return rc;
-        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n2w, L.n2b, (f32res || last) ? xo32 : nullptr, xo16, s))) return rc;
+        // norm2; Q8: with the next layer's QKV activation codes
+        if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n2w, L.n2b,
+                             (f32res || last) ? xo32 : nullptr, xo16, s, q8 && !last)))
+            return rc;
     }
 
     // pooling → Matryoshka → L2 (model.go:417-453)

@@ -175,12 +175,17 @@ constexpr int ATTN_ONE_BLOCK_KEYS = 128;
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
 // gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
 // binary16 sum to x16 instead, for a consumer that folds this LayerNorm.
+// q non-null (with gamma and x32): also the int8 codes and scales of the
+// normalized rows, as quantize_rows would compute them from x32 (T = total
+// rows, for the separate pass the generic kernel needs).
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
-                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s);
-// y32 or y16 (exactly one non-null) holds proj + bias + residual.
+                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s, int8_t *q = nullptr,
+                    float *qs = nullptr, int T = 0);
+// y32 or y16 (exactly one non-null) holds proj + bias + residual; q
+// non-null (with x32): also the normalized rows' int8 codes and scales.
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
-                      float eps, float *x32, f16 *x16, hipStream_t s);
+                      float eps, float *x32, f16 *x16, hipStream_t s, int8_t *q = nullptr, float *qs = nullptr);
 // (mean, rstd) of each binary16 row of y [M, H] (H in {256, 384, 512, 768,
 // 1024}): float64 Σy and Σy², rounded to float32 like layerNormRows' float64
 // statistics.

@@ -3,16 +3,19 @@
 // (native/kernel.go:26-43) with the same epilogues as gemm.hip (bias, GELU,
 // residual, the folded-LayerNorm modes).
 //
-// Layout and schedule:
-// * One 512-thread block per CU, looping over 256×128 output tiles; each of
-//   the 8 XCDs owns a contiguous range of tiles, so an A row panel is fetched
-//   into one XCD's L2 and reused there by all of that panel's column tiles.
-// * Operands stream into a 3-slot LDS ring (48 KB per 64-wide K slice)
-//   straight from global memory with buffer_load … lds (no VGPR staging, no
-//   LDS store instructions).  The ring runs across tile boundaries: the next
-//   tile's first slices are in flight during the current tile's last slice
-//   and its epilogue.  Rows past M read as zero through the buffer range
-//   check.
+// Layout and schedule (the default configuration, R2 below; the others are
+// tuning alternatives):
+// * Two persistent 4-wave blocks per CU, each looping over 128×128 output
+//   tiles (a wave owns 64×64); each of the 8 XCDs owns a contiguous range of
+//   tiles, so an A row panel is fetched into one XCD's L2 and reused there
+//   by all of that panel's column tiles.
+// * Operands stream into a 2-slot LDS ring (32 KB per 64-wide K slice per
+//   block) straight from global memory with buffer_load … lds (no VGPR
+//   staging, no LDS store instructions).  The ring runs across tile
+//   boundaries: the next tile's first slice is in flight during the current
+//   tile's last slice and its epilogue, and while one block waits at its
+//   barrier the other keeps the matrix cores busy.  Rows past M read as zero
+//   through the buffer range check.
 // * LDS rows are 128 bytes with the 16-byte chunk index XOR-ed with row%8,
 //   which makes the MFMA fragment reads (16 rows × one chunk) conflict-free.
 // * v_mfma_f32_16x16x32_f16 with the weight fragment as the A operand: a

@@ -203,6 +203,43 @@ __device__ __forceinline__ void st_row(float *o32, f16 *o16, int lane, const flo
     }
 }
 
+// Per-row int8 codes of a row held in ld_row's layout (quantizeRowQ8,
+// native/quant.go:42-70, as the activation quantizer of matMulTQ8,
+// quant.go:104-110): scale = float32(amax)/127; code =
+// round-half-away(float64(v)·(127/float64(amax))) clamped to ±127; a zero
+// row gives zero codes and scale 0.  Four codes per 32-bit store.
+template <int VPL>
+__device__ __forceinline__ void quant_row_v(const float (&v)[VPL], int lane, int8_t *q, float *scale) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = wave_max(amax);
+    const double inv = amax == 0.f ? 0.0 : 127.0 / (double)amax;
+    auto code = [&](float x) -> uint32_t {
+        const double c = fmin(127.0, fmax(-127.0, round((double)x * inv)));
+        return (uint32_t)(uint8_t)(int8_t)(int)c;
+    };
+    constexpr int N4 = VPL / 4;
+#pragma unroll
+    for (int c = 0; c < N4; ++c)
+        *(uint32_t *)(q + 4 * (64 * c + lane)) =
+            code(v[4 * c]) | code(v[4 * c + 1]) << 8 | code(v[4 * c + 2]) << 16 | code(v[4 * c + 3]) << 24;
+    if (VPL % 4) *(uint16_t *)(q + 256 * N4 + 2 * lane) = (uint16_t)(code(v[4 * N4]) | code(v[4 * N4 + 1]) << 8);
+    if (lane == 0) *scale = amax == 0.f ? 0.f : __fdiv_rn(amax, 127.0f);
+}
+
+// One row per wave, held in registers between the absmax and the codes.
+template <int VPL>
+__global__ __launch_bounds__(256) void quantize_rows_v_kernel(const float *x, int M, int ldx, int8_t *q,
+                                                              float *scale) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int lane = threadIdx.x & 63;
+    float v[VPL];
+    ld_row<VPL>(x + (size_t)row * ldx, lane, v);
+    quant_row_v<VPL>(v, lane, q + (size_t)row * (64 * VPL), scale + row);
+}
+
 // Normalizes v in place with statistics of the row and writes it out; gw/gb
 // hold this lane's γ/β elements.
 template <int VPL>
@@ -248,9 +285,12 @@ __global__ __launch_bounds__(256) void row_stats_kernel(const f16 *y, int M, flo
 
 // Two rows per wave: both rows and γ/β are requested before any reduction,
 // so one memory latency covers the pair.
+// q non-null: also the int8 codes and scale of each normalized row (the
+// activation quantizer of the next int8 GEMM, quant_row_v).
 template <int VPL, class T>
 __global__ __launch_bounds__(256) void layer_norm_v_kernel(const T *y, int M, const float *gamma,
-                                                           const float *beta, float eps, float *x32, f16 *x16) {
+                                                           const float *beta, float eps, float *x32, f16 *x16,
+                                                           int8_t *q, float *qs) {
     constexpr int H = 64 * VPL;
     const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
     if (row >= M) return;
@@ -262,15 +302,18 @@ __global__ __launch_bounds__(256) void layer_norm_v_kernel(const T *y, int M, co
     ld_row<VPL>(gamma, lane, gw);
     ld_row<VPL>(beta, lane, gb);
     ln_row_v<VPL>(v0, gw, gb, eps, x32 ? x32 + (size_t)row * H : nullptr, x16 ? x16 + (size_t)row * H : nullptr);
-    if (two)
+    if (q) quant_row_v<VPL>(v0, lane, q + (size_t)row * H, qs + row);
+    if (two) {
         ln_row_v<VPL>(v1, gw, gb, eps, x32 ? x32 + (size_t)(row + 1) * H : nullptr,
                       x16 ? x16 + (size_t)(row + 1) * H : nullptr);
+        if (q) quant_row_v<VPL>(v1, lane, q + (size_t)(row + 1) * H, qs + row + 1);
+    }
 }
 template <int VPL>
 __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, const int32_t *offsets,
                                                          const float *word, const float *type0, const float *pos,
                                                          const float *gamma, const float *beta, float eps,
-                                                         float *x32, f16 *x16) {
+                                                         float *x32, f16 *x16, int8_t *q, float *qs) {
     constexpr int H = 64 * VPL;
     const int seq = blockIdx.y;
     const int start = offsets[seq], L = offsets[seq + 1] - start;
@@ -298,6 +341,7 @@ __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, con
     ld_row<VPL>(gamma, lane, gw);
     ld_row<VPL>(beta, lane, gb);
     ln_row_v<VPL>(v, gw, gb, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
+    if (q) quant_row_v<VPL>(v, lane, q + row * H, qs + row);
 }
 
 __device__ double block_sum_f64(double v, double *red) {
@@ -401,12 +445,13 @@ __global__ __launch_bounds__(256) void pool_kernel(const float *x32, const float
 namespace fh {
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
-                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s) {
+                    const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s, int8_t *q,
+                    float *qs, int T) {
     if (nseq <= 0) return hipSuccess;
     const dim3 grid((max_len + 3) / 4, nseq);
 #define FH_EMB_V(V)                                                                                          \
     case V: hipLaunchKernelGGL(embed_ln_v_kernel<V>, grid, dim3(256), 0, s, ids, offsets, word, type0, pos, gamma, \
-                               beta, eps, x32, x16);                                                         \
+                               beta, eps, x32, x16, gamma ? q : nullptr, qs);                                \
         return hipGetLastError();
     if (H % 64 == 0) {
         switch (H / 64) {
@@ -417,18 +462,19 @@ hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int ma
 #undef FH_EMB_V
     hipLaunchKernelGGL(embed_ln_kernel, grid, dim3(256), 0, s, ids, offsets, word, type0, pos, gamma, beta, eps, H,
                        x32, x16);
+    if (q && x32) return quantize_rows(x32, T, H, H, q, qs, s);
     return hipGetLastError();
 }
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,
-                      float eps, float *x32, f16 *x16, hipStream_t s) {
+                      float eps, float *x32, f16 *x16, hipStream_t s, int8_t *q, float *qs) {
     if (M <= 0) return hipSuccess;
     const dim3 grid((M + 3) / 4), grid2((M + 7) / 8);
 #define FH_LN_V(V)                                                                                             \
     case V:                                                                                                    \
         if (y16) hipLaunchKernelGGL((layer_norm_v_kernel<V, f16>), grid2, dim3(256), 0, s, y16, M, gamma, beta, eps, \
-                                    x32, x16);                                                                 \
+                                    x32, x16, q, qs);                                                          \
         else hipLaunchKernelGGL((layer_norm_v_kernel<V, float>), grid2, dim3(256), 0, s, y32, M, gamma, beta, eps, \
-                                x32, x16);                                                                     \
+                                x32, x16, q, qs);                                                              \
         return hipGetLastError();
     if (H % 64 == 0 && gamma) {
         switch (H / 64) {
@@ -439,6 +485,10 @@ hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const floa
 #undef FH_LN_V
     if (y16) hipLaunchKernelGGL(layer_norm_kernel<f16>, grid, dim3(256), 0, s, y16, M, H, gamma, beta, eps, x32, x16);
     else hipLaunchKernelGGL(layer_norm_kernel<float>, grid, dim3(256), 0, s, y32, M, H, gamma, beta, eps, x32, x16);
+    if (q) {
+        if (!x32) return hipErrorInvalidValue;
+        return quantize_rows(x32, M, H, H, q, qs, s);
+    }
     return hipGetLastError();
 }
 hipError_t row_stats(const f16 *y, int M, int H, float eps, f32x2 *st, hipStream_t s) {
@@ -463,6 +513,16 @@ hipError_t gather_rows(const float *x32, const f16 *x16, const f32x2 *st, const 
 hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float *scale,
                          hipStream_t s) {
     if (M <= 0) return hipSuccess;
+#define FH_Q_V(V)                                                                                           \
+    case V: hipLaunchKernelGGL(quantize_rows_v_kernel<V>, dim3((M + 3) / 4), dim3(256), 0, s, x, M, ldx, q, scale); \
+        return hipGetLastError();
+    if (K % 64 == 0 && ldx % 4 == 0) {
+        switch (K / 64) {
+            FH_Q_V(4) FH_Q_V(6) FH_Q_V(8) FH_Q_V(12) FH_Q_V(16) FH_Q_V(24) FH_Q_V(32) FH_Q_V(48)
+        default: break;
+        }
+    }
+#undef FH_Q_V
     hipLaunchKernelGGL(quantize_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, M, K, ldx, q, scale);
     return hipGetLastError();
 }

@@ -154,10 +154,11 @@ def test_nomic_2048_tokens():
 
 
 def test_mixed_lengths_scheduled_by_class():
-    """A batch mixing short (≤ 128-token) and long sequences is run as one
-    forward per attention class: every vector equals its single-sequence
-    forward bit for bit (native/model_test.go:165-197), in any batch order,
-    and meets the gate against the oracle."""
+    """A batch mixing short (≤ 128-token) and long sequences runs sorted
+    longest first, with attention launched once per length class: every
+    vector equals its single-sequence forward bit for bit
+    (native/model_test.go:165-197), in any batch order, and meets the gate
+    against the oracle."""
     w = synth.workload("minilm-l6")
     m, tensors = _model(w)
     rng = np.random.default_rng(21)
@@ -285,3 +286,46 @@ def test_fp16_pack_on_device(tmp_path):
     _check("minilm-l6", a, want, "minilm-l6 F16 pack")
     m16.close()
     m32.close()
+
+
+def _stress_tensors(w, seed=77):
+    """bge-small-shaped weights with the features of real BERT checkpoints
+    that synthetic N(0, 0.02) weights lack: a few outlier channels with
+    large LayerNorm γ and β (every norm), so the residual stream carries
+    channels 10-30x larger than the rest; an embedding DC offset (every
+    token shares a large per-channel vector), so rows have a mean far from
+    zero; larger attention/FFN weights (std 0.05)."""
+    t = synth.make_tensors(w.config, w.weight_seed + seed, std=0.05)
+    rng = np.random.default_rng(seed)
+    H = w.config["hidden_size"]
+    out_ch = rng.choice(H, 4, replace=False)
+    for name in list(t):
+        if name.endswith("norm.weight") or name.endswith("norm1.weight") or name.endswith("norm2.weight"):
+            t[name][out_ch] = np.float32([12.0, -9.0, 20.0, 7.5])
+        if name.endswith("norm.bias") or name.endswith("norm1.bias") or name.endswith("norm2.bias"):
+            t[name][out_ch] = np.float32([3.0, -2.5, 5.0, 1.5])
+    dc = (rng.standard_normal(H) * 0.5).astype(np.float32)
+    dc[out_ch] += np.float32([4.0, -3.0, 6.0, 2.0])
+    t["embeddings.word"] = (t["embeddings.word"] + dc).astype(np.float32)
+    return t, out_ch
+
+
+def test_stress_pack_outlier_channels():
+    """The binary16 residual stream and the LayerNorm fold
+    (rstd·(y·W'ᵀ − mean·c1) + c2) against the oracle on a pack with outlier
+    channels and a DC offset, at the bench's kernel routing (ring GEMM +
+    fused layer tail) and at a small batch (tiled GEMMs)."""
+    w = synth.workload("bge-small")
+    tensors, out_ch = _stress_tensors(w)
+    m, _ = _model(w, tensors)
+    om = oracle.Model(w.config, tensors)
+    keep = np.setdiff1d(np.arange(w.config["hidden_size"]), out_ch)
+    for B, seed in ((192, 31), (12, 32)):
+        ids, offsets = synth.make_batch(w.ids_seed + seed, B, 16, 128)
+        got = m.EncodePacked(ids, offsets)
+        want = om.encode_batch(ids, offsets, 0, threads=THREADS)
+        _check("bge-small-stress", got, want, f"bge-small stress pack (outlier channels, DC offset) B={B}")
+        # the outlier channels dominate the pooled vector: the rest must meet
+        # the gate on its own
+        _check("bge-small-stress", got[:, keep], want[:, keep], f"  same, the {keep.size} non-outlier channels")
+    m.close()

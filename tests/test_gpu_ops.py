@@ -442,13 +442,18 @@ def test_gemm_swiglu_interleave(M, I, K):
     np.testing.assert_allclose(got, ref, atol=3e-4 * math.sqrt(K), rtol=1e-4)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 4, 16), (7, 16, 48), (37, 96, 384), (300, 1152, 384), (65, 384, 1536)])
+@pytest.mark.parametrize("M,N,K", [(1, 4, 16), (7, 16, 48), (37, 96, 384), (300, 1152, 384), (65, 384, 1536),
+                                   (9, 64, 768), (5, 32, 3072)])
 def test_q8_quantize_and_gemm_bit_exact(M, N, K):
     """Activation codes, scales and the i8 GEMM equal the oracle's Q8 path
-    (native/quant.go:42-137) bit for bit."""
+    (native/quant.go:42-137) bit for bit, including codes at exact halves
+    (rounded away from zero, as math.Round)."""
     rng = np.random.default_rng(N + K)
     a = rng.standard_normal((M, K)).astype(np.float32)
     a[0, :] = 0.0  # all-zero row: scale 0, zero codes
+    if M > 2:  # row 1: amax 127, then ±(k + 0.5) exactly
+        a[1, :] = ((np.arange(K) % 120) + 0.5) * np.where(np.arange(K) % 2, -1.0, 1.0)
+        a[1, 0] = 127.0
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32)
     qb, sb = oracle.quantize_q8(w)
