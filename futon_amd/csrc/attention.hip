@@ -161,8 +161,39 @@ void attn_kernel(AttnArgs a) {
     const int chunks = d >> 3;  // 16-byte chunks per row (d % 8 == 0)
     const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
 
+    // ── Q fragments (B operand of Sᵀ = K·Qᵀ): lane holds dims
+    //    [dk·32 + (lane/16)·8, +8) of query lane%16 of each tile (load_q's
+    //    arithmetic, written out here: this kernel's register allocation
+    //    spills with the shared helper). ──
     f16x8 qf[QT][D / 32];
-    load_q<D, QT, ROPE>(a, start, L, q0 + wave * QT * 16, lane, qf, head);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int q = min(q0 + (wave * QT + qt) * 16 + (lane & 15), L - 1);
+        const f16 *qrow = a.qkv + (size_t)(start + q) * ld + head * d;
+#pragma unroll
+        for (int dk = 0; dk < D / 32; ++dk) {
+            const int j0 = dk * 32 + (lane >> 4) * 8;
+            f16x8 v = z8;
+            if (j0 < d) v = *(const f16x8 *)(qrow + j0);
+            if (ROPE && j0 < d) {
+                f16x8 p = v;
+                if (half >= 8) p = *(const f16x8 *)(qrow + (j0 < half ? j0 + half : j0 - half));
+                f16x8 r;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = j0 + e;
+                    const int i = j < half ? j : j - half;  // table index
+                    const float cs = a.rope_cos[q * half + i], sn = a.rope_sin[q * half + i];
+                    float partner;
+                    if (half >= 8) partner = (float)p[e];
+                    else partner = (float)v[(e + half) & 7];
+                    r[e] = (f16)rot((float)v[e], partner, cs, sn, j < half);
+                }
+                v = r;
+            }
+            qf[qt][dk] = v;
+        }
+    }
 
     f32x4 o[QS][D / 16];
     float m_run[QS], l_run[QS];

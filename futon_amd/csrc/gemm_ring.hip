@@ -98,14 +98,31 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     bool isA[DPW];
 #pragma unroll
     for (int i = 0; i < DPW; ++i) isA[i] = (wave * DPW + i) * 8 < BM;
-    // Issues slice s of this block's sequence (past the end: the last slice
-    // again, into a slot nobody reads) into slot s % SLOTS.
-    auto issue = [&](int s) {
-        const int sc = min(s, nsl - 1);
-        const int ti = sc / nk, kk = sc - ti * nk;
-        const int t = t0 + ti * nbx;
-        const int mt = t / ntn, nt = t - mt * ntn;
-        const uint32_t slot = ring0 + (uint32_t)(s % SLOTS) * STAGE;
+    // Issues the next slice of this block's sequence (past the end: the last
+    // slice again, into a slot nobody reads) into the next slot.  Slices are
+    // issued in order, so the slice's tile and K position advance by
+    // counting, not by dividing: integer division is a long scalar sequence
+    // that would delay the waves' matrix instructions every slice.
+    int is_kk = 0, is_left = nsl, is_slot = 0, is_mt, is_nt;
+    {
+        is_mt = t0 / ntn;
+        is_nt = t0 - is_mt * ntn;
+    }
+    auto issue = [&] {
+        const int kk = is_kk, mt = is_mt, nt = is_nt;
+        const uint32_t slot = ring0 + (uint32_t)is_slot * STAGE;
+        is_slot = is_slot + 1 == SLOTS ? 0 : is_slot + 1;
+        if (is_left > 1) {  // advance to the following slice (the last one is repeated)
+            --is_left;
+            if (++is_kk == nk) {
+                is_kk = 0;
+                is_nt += nbx;  // the next tile of this block: t + nbx
+                while (is_nt >= ntn) {
+                    is_nt -= ntn;
+                    ++is_mt;
+                }
+            }
+        }
         const uint32_t soff = (uint32_t)kk * ROWB;
         const uint32_t offA = (uint32_t)(mt * BM) * lda_b + lrow * lda_b + lchunk;
         const uint32_t offB = (uint32_t)(nt * BN - BM) * ldb_b + lrow * ldb_b + lchunk;
@@ -275,23 +292,31 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     // enough: n counts at most one epilogue.
     constexpr int NIN = (SLOTS - 2) * DPW;
 #pragma unroll
-    for (int i = 0; i < SLOTS - 1; ++i) issue(i);
+    for (int i = 0; i < SLOTS - 1; ++i) issue();
+    // kk: K position of slice s in its tile; since_end: slices since the
+    // last tile end (an epilogue's stores are outstanding for the next
+    // SLOTS − 1 slices).
+    int kk = 0, ti = 0, slot = 0, since_end = SLOTS;
     for (int s = 0; s < nsl; ++s) {
-        bool after_epi = false;
-#pragma unroll
-        for (int jj = 1; jj < SLOTS; ++jj) after_epi |= s >= jj && (s - jj + 1) % nk == 0;
-        if (after_epi) {
+        if (since_end < SLOTS) {
             asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NIN + NSTORE) : "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NIN) : "memory");
         }
-        const bool tile_end = (s + 1) % nk == 0;
-        if (tile_end) epi_load(s / nk);
-        issue(s + SLOTS - 1);
-        compute(s % SLOTS);
+        const bool tile_end = kk == nk - 1;
+        if (tile_end) epi_load(ti);
+        issue();
+        compute(slot);
+        slot = slot + 1 == SLOTS ? 0 : slot + 1;
+        ++since_end;
         if (tile_end) {
-            epi_store(s / nk);
+            epi_store(ti);
             clear();
+            kk = 0;
+            ++ti;
+            since_end = 1;
+        } else {
+            ++kk;
         }
     }
     // The DMA path writes this block's LDS: drain it before the block ends.
