@@ -20,6 +20,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfuton_hip.so")
+CLI = os.path.join(HERE, "futon_embed")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
@@ -73,8 +74,16 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libfuton_hip.so failed")
     os.replace(tmp, LIB)
+    # The `futon embed` command on this library (csrc/cli/futon_embed.cpp).
+    cmd = [CXX, *HOST_FLAGS, os.path.join(CSRC, "cli", "futon_embed.cpp"), "-o", CLI + ".tmp", "-L", HERE,
+           "-lfuton_hip", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("build of futon_embed failed")
+    os.replace(CLI + ".tmp", CLI)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {CLI}")
     return LIB
 
 
