@@ -52,6 +52,41 @@ bool long_pipeline() {
 template <int D, int WAVES, bool ONE>
 constexpr int attn_min_waves() { return (ONE && D == 32 && WAVES >= 4) ? ATTN_ONE_WAVES : 1; }
 
+// Cross-row reductions of a lane's value with lane l^16 / l^32 through
+// gfx950's row-swap permutes (no LDS crossbar, unlike ds_bpermute): with
+// both operands x, permlane16_swap returns {x[l], x[l^16]} in every lane and
+// permlane32_swap {x[l], x[l^32]}, so max and sum of the pair are what
+// __shfl_xor would give, bit for bit (both operations are commutative).
+// Operands and results pass through empty asm statements: this compiler
+// otherwise folds a float max or sum of the two results as if both were the
+// first (it drops the operation).
+template <int ROWS>
+__device__ __forceinline__ f32x2 swap_pair(float v) {
+    unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+    asm volatile("" : "+v"(b));
+    const auto r = ROWS == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                              : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    unsigned r0 = r[0], r1 = r[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    return (f32x2){__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
+}
+__device__ __forceinline__ float max_xor16(float v) {
+    const f32x2 p = swap_pair<16>(v);
+    return fmaxf(p[0], p[1]);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const f32x2 p = swap_pair<32>(v);
+    return fmaxf(p[0], p[1]);
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const f32x2 p = swap_pair<16>(v);
+    return p[0] + p[1];
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const f32x2 p = swap_pair<32>(v);
+    return p[0] + p[1];
+}
+
 // Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
 // contiguous range of (query group, head, sequence) items, ordered so that
 // blocks which read the same qkv lines share one L2 (the lines are then
@@ -320,8 +355,7 @@ void attn_kernel(AttnArgs a) {
                 }
                 mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_xor32(max_xor16(mx));
             const float m_new = fmaxf(m_run[st], mx * sl2);  // log2-scaled running max
             const float corr = __builtin_amdgcn_exp2f(m_run[st] - m_new);
             float psum = 0.f;
@@ -334,8 +368,7 @@ void attn_kernel(AttnArgs a) {
                     psum += p;
                     pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
                 }
-            psum += __shfl_xor(psum, 16, 64);
-            psum += __shfl_xor(psum, 32, 64);
+            psum = sum_xor32(sum_xor16(psum));
             l_run[st] = l_run[st] * corr + psum;
             m_run[st] = m_new;
 #pragma unroll
@@ -511,8 +544,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
             }
             mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_xor32(max_xor16(mx));
         const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
         const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
         float psum = 0.f;
@@ -525,8 +557,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
                 psum += p;
                 pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
             }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = sum_xor32(sum_xor16(psum));
         l_run[qt] = l_run[qt] * corr + psum;
         m_run[qt] = m_new;
 #pragma unroll
