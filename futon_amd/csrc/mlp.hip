@@ -22,10 +22,13 @@
 //   its epilogue (LayerNorm fold, GELU, rounding to binary16) writes h into
 //   LDS; after one barrier, phase 2 accumulates outputs 48w .. 48w+47 over
 //   the chunk's 128 features.  h is double-buffered, so that barrier is the
-//   chunk's only one, and each chunk's epilogue (the VALU-heavy part) is
-//   split between the previous chunk's phase 2 and the next chunk's phase 1,
-//   so the matrix and vector units work side by side.  The fold terms c1/c2
-//   are staged in LDS once per block.
+//   chunk's only one, and each chunk's epilogue (the VALU-heavy part) runs
+//   interleaved with the previous chunk's phase 2.  The fold terms c1/c2 are
+//   staged in LDS once per block.
+// * On gfx950 a wave64 VALU instruction issued beside the MFMA stream hides
+//   under it only about once per MFMA, so this kernel's time is close to its
+//   MFMA time plus its vector time; what pays is fewer vector instructions
+//   and no exposed memory latency, not where the vector work is placed.
 // The accumulation orders over K and the epilogue arithmetic are those of the
 // ring GEMM's LN_IN/GELU and RES_LN forms, so the result has the same bits as
 // the two separate GEMMs.
@@ -53,6 +56,8 @@ constexpr int NT1 = fh::MLP_NT1;            // phase-1 feature tiles per wave
 constexpr int NT2 = fh::MLP_NT2;            // phase-2 output tiles per wave
 constexpr int ROWB = 128;               // bytes per LDS row (64 binary16)
 constexpr int MT_MAX = 5;
+constexpr int PW = 6;                   // Wo k-steps held in registers (phase 0)
+constexpr int QD = 4;                   // Wq k-steps held in registers (QKV passes)
 constexpr int I_MAX = 2048;             // widest intermediate layer (fold terms staged in LDS)
 constexpr int W1C = NW * KS1 * NT1 * 64;  // 16-byte units of W1 per chunk
 constexpr int W2C = NW * KS2 * NT2 * 64;  // 16-byte units of W2 per chunk
@@ -73,7 +78,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     constexpr int O_OFF = A_BYTES, R_BYTES = 2 * H_BYTES > A_BYTES ? 2 * H_BYTES : A_BYTES;
     constexpr int C_OFF = A_BYTES + R_BYTES;        // c1 [I_MAX] then c2 [I_MAX] (f32)
     constexpr int S_OFF = C_OFF + 2 * I_MAX * 4;
-    constexpr int TS = MT;                          // epilogue tiles done beside phase 2 (all)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S_OFF + BM * 8];
     const uint8_t *const atile = lds;
     const float *const lc1 = (const float *)(lds + C_OFF), *const lc2 = lc1 + I_MAX;
@@ -143,28 +147,43 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     int fo[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) fo[k] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * k) ^ (lane & 7)) << 4);
+    // MFMA B fragments of k-step k of a resident [BM, 384] tile: one b128
+    // per 16-token group.
+    auto load_tile_frags = [&](i32x4(&f)[MT], const uint8_t *tile, int k) {
+        const uint8_t *ab = tile + (k >> 1) * BM * ROWB + fo[k & 1];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) f[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+    };
 
     if constexpr (OUTP) {
         // Phase 0, the attention output projection (the out-projection GEMM's
         // RES_LN form, same K order and epilogue arithmetic): the attention
-        // tile goes to region R, Wo fragments stream through registers four
+        // tile goes to region R, Wo fragments stream through registers PW
         // k-steps ahead, and yB = attn·Woᵀ + bo + LN_a(ya) is written in
-        // binary16 into the token tile.  This lane's outputs: the same
-        // n0 + {0..4·NT2−1} as the final epilogue.  Everything the phase
-        // reads from memory (the tile, the first Wo fragments, ya and its
-        // statistics, bo/γ/β) and the fold terms for later are requested
-        // before the first wait, so their latencies overlap.
+        // binary16 into the token tile, over ya, which was transferred
+        // there.  This lane's outputs: the same n0 + {0..4·NT2−1} as the
+        // final epilogue.
+        // Issue order: the attention tile, the first PW k-steps of Wo, then
+        // ya, the fold terms, bo/γ/β and ya's statistics.  vmcnt retires in
+        // issue order, so waiting until no more than the Wo loads and the
+        // smallest per-wave count of ya transfers remain outstanding means
+        // this wave's attention transfers have landed; the rest lands under
+        // the products (the compiler waits for register loads before their
+        // use; the empty asm statements keep the groups in this order).
         dma_tile(g.attn, lds0 + O_OFF);
-        dma_fold_terms();
+        asm volatile("" ::: "memory");
         const i32x4 *w0p = (const i32x4 *)g.wo + (size_t)wave * KS2 * NT2 * 64 + lane;
-        i32x4 w0f[KS2][NT2];
+        i32x4 w0f[PW][NT2];
+        auto wo_frag = [&](int k, int t) { return w0p[(size_t)(k / KS2) * W2C + ((k % KS2) * NT2 + t) * 64]; };
 #pragma unroll
-        for (int ks = 0; ks < KS2; ++ks)
+        for (int ks = 0; ks < PW; ++ks)
 #pragma unroll
-            for (int t = 0; t < NT2; ++t) w0f[ks][t] = w0p[(ks * NT2 + t) * 64];
+            for (int t = 0; t < NT2; ++t) w0f[ks][t] = wo_frag(ks, t);
+        asm volatile("" ::: "memory");
+        dma_tile(g.ya, lds0);
+        dma_fold_terms();
         const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
         f32x4 kb[NT2], kg[NT2], kt[NT2];
-        f16x4 ya4[MT][NT2];
         f32x2 sa[MT];
 #pragma unroll
         for (int t = 0; t < NT2; ++t) {
@@ -173,33 +192,34 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             kt[t] = *(const f32x4 *)(g.ba + n0 + 4 * t);
         }
 #pragma unroll
-        for (int tm = 0; tm < MT; ++tm) {
-            const int row = min(m0 + tm * 16 + (lane & 15), g.M - 1);
-            sa[tm] = g.stats_a[row];
-#pragma unroll
-            for (int t = 0; t < NT2; ++t) ya4[tm][t] = *(const f16x4 *)(g.ya + (size_t)row * HD + n0 + 4 * t);
-        }
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        for (int tm = 0; tm < MT; ++tm) sa[tm] = g.stats_a[min(m0 + tm * 16 + (lane & 15), g.M - 1)];
+        constexpr int AFTER = NT2 * PW + 12 * MT / NW;  // issued after the last attention transfer, at least
+        static_assert(AFTER <= 63, "vmcnt immediate");
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(AFTER) : "memory");
         f32x4 acc0[NT2][MT];
+        i32x4 af0[2][MT];
+        load_tile_frags(af0[0], lds + O_OFF, 0);
 #pragma unroll
         for (int k = 0; k < KS1; ++k) {
-            const uint8_t *ab = lds + O_OFF + (k >> 1) * BM * ROWB + fo[k & 1];
-            i32x4 af[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+            if (k + 1 < KS1) load_tile_frags(af0[(k + 1) & 1], lds + O_OFF, k + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const i32x4(&af)[MT] = af0[k & 1];
 #pragma unroll
             for (int t = 0; t < NT2; ++t) {
 #pragma unroll
                 for (int tm = 0; tm < MT; ++tm)
                     acc0[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        __builtin_bit_cast(f16x8, w0f[k % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
+                        __builtin_bit_cast(f16x8, w0f[k % PW][t]), __builtin_bit_cast(f16x8, af[tm]),
                         k == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc0[t][tm], 0, 0, 0);
-                if (k + KS2 < KS1) {
-                    const int kn = k + KS2;
-                    w0f[k % KS2][t] = w0p[(size_t)(kn / KS2) * W2C + ((kn % KS2) * NT2 + t) * 64];
-                }
+                if (k + PW < KS1) w0f[k % PW][t] = wo_frag(k + PW, t);
             }
         }
+        // The block's weights are requested now, to land under the epilogue
+        // and the statistics; ya's transfers are waited for (every wave's).
+        asm volatile("" ::: "memory");
+        prefetch_w();
+        constexpr int NPF = W1H * NT1 + KS2 * NT2;  // the loads of prefetch_w
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NPF) : "memory");
 #pragma unroll
         for (int tm = 0; tm < MT; ++tm) {
             const int r = tm * 16 + (lane & 15);
@@ -208,17 +228,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 const int n = n0 + 4 * t;
                 f32x4 x = acc0[t][tm];
                 if (g.bo) x += kb[t];
-                x += ln_resid_v(ya4[tm][t], sa[tm], kg[t], kt[t]);
+                f16x4 *const p = (f16x4 *)(lds + (n >> 6) * BM * ROWB + r * ROWB + ((((n & 63) >> 3) ^ (lane & 7)) << 4) +
+                                           (n & 7) * 2);
+                x += ln_resid_v(*p, sa[tm], kg[t], kt[t]);
                 f16x4 o;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
-                *(f16x4 *)(lds + (n >> 6) * BM * ROWB + r * ROWB + ((((n & 63) >> 3) ^ (lane & 7)) << 4) +
-                           (n & 7) * 2) = o;
+                *p = o;
             }
         }
-        // yB is complete; the weights of the block proper follow.
+        // yB is complete.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        prefetch_w();
     } else {
         prefetch_w();
         dma_tile(g.y, lds0);
@@ -256,7 +276,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // Chunk-local phase-1 features of this lane: fl .. fl + 4·NT1 − 1.
     const int fl = wave * 16 * NT1 + (lane >> 4) * 4 * NT1;
 
-    f32x4 accA[NT1][MT], accB[NT1][MT], acc2[NT2][MT];
+    f32x4 acc1[NT1][MT], acc2[NT2][MT];  // phase-1 product of one chunk, the block's output
 #pragma unroll
     for (int tm = 0; tm < MT; ++tm)
 #pragma unroll
@@ -318,29 +338,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         }
     };
 
-    // Chunk 0's phase 1 and the first part of its epilogue; its W1 registers
-    // are refilled with chunk 1's fragments.
-    p1_chunk(0, accA);
+    // Chunk 0's phase 1 and its epilogue; its W1 registers are refilled with
+    // chunk 1's fragments.
+    p1_chunk(0, acc1);
 #pragma unroll
-    for (int tm = 0; tm < TS; ++tm) epi1_tm(tm, accA, 0);
+    for (int tm = 0; tm < MT; ++tm) epi1_tm(tm, acc1, 0);
 
-    // Chunk j: stage A multiplies chunk j+1's phase 1 into accN (refilling
-    // W1 with chunk j+2's fragments) beside the rest of chunk j's epilogue
-    // (accC); one barrier; stage B multiplies chunk j's phase 2 (refilling W2
-    // with chunk j+1's) beside the first part of chunk j+1's epilogue.  h is
-    // double-buffered: chunk j+1's h goes to the buffer chunk j−1 used, read
-    // by every wave before it passed this chunk's barrier.  MORE (compile
-    // time, so neither stage branches): chunk j+1 exists.  In stage B the
-    // epilogue's VALU work is interleaved with the products (one MFMA, then a
-    // share of the epilogue), so that the two overlap.
-    auto chunk = [&](int j, f32x4(&accC)[NT1][MT], f32x4(&accN)[NT1][MT], auto more_c) {
+    // Chunk j: stage A multiplies chunk j+1's phase 1 into accN (refilling W1
+    // with chunk j+2's fragments); one barrier (chunk j's h is complete);
+    // stage B multiplies chunk j's phase 2 (refilling W2 with chunk j+1's)
+    // beside chunk j+1's epilogue, interleaved with the products (one MFMA,
+    // then a share of the epilogue).  h is double-buffered: chunk j+1's h goes
+    // to the buffer chunk j−1 used, read by every wave before it passed this
+    // chunk's barrier.  MORE (compile time, so neither stage branches): chunk
+    // j+1 exists.  (Moving part of the epilogue into stage A measured no
+    // faster: MFMA and VALU issue share the SIMD, so where the vector work
+    // sits matters less than how much of it there is.)
+    auto chunk = [&](int j, f32x4(&accN)[NT1][MT], auto more_c) {
         constexpr bool MORE = decltype(more_c)::value;
-        if constexpr (MORE) {
-            p1_chunk(j + 1, accN);
-        } else {
-#pragma unroll
-            for (int tm = TS; tm < MT; ++tm) epi1_tm(tm, accC, j);
-        }
+        if constexpr (MORE) p1_chunk(j + 1, accN);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const uint8_t *hb = lds + A_BYTES + (j & 1) * H_BYTES;
         const size_t next2 = (size_t)min(j + 1, nchunk - 1) * W2C;
@@ -358,11 +374,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             }
             if constexpr (MORE) {
 #pragma unroll
-                for (int tm = ks * TS / KS2; tm < (ks + 1) * TS / KS2; ++tm) epi1_tm(tm, accN, j + 1);
+                for (int tm = ks * MT / KS2; tm < (ks + 1) * MT / KS2; ++tm) epi1_tm(tm, accN, j + 1);
                 // One epilogue tile is ~80 VALU instructions: spread them
                 // between the k-step's NT2·MT products (groups of one MFMA and
                 // a share of the VALU work; the counts must be constants).
-                const int ntile = (ks + 1) * TS / KS2 - ks * TS / KS2;
+                const int ntile = (ks + 1) * MT / KS2 - ks * MT / KS2;
                 if (ntile == 1) {
 #pragma unroll
                     for (int i = 0; i < NT2 * MT; ++i) {
@@ -380,29 +396,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         }
     };
     int j = 0;
-    for (; j + 2 < nchunk; j += 2) {
-        chunk(j, accA, accB, std::true_type{});
-        chunk(j + 1, accB, accA, std::true_type{});
-    }
-    if (j + 1 < nchunk) {
-        chunk(j, accA, accB, std::true_type{});
-        chunk(j + 1, accB, accA, std::false_type{});
-    } else {
-        chunk(j, accA, accB, std::false_type{});
-    }
+    for (; j + 1 < nchunk; ++j) chunk(j, acc1, std::true_type{});
+    chunk(j, acc1, std::false_type{});
 
     // The next layer's Wq fragments (k-step kg of the 3·KS1-step stream over
-    // the three 384-row blocks, tile t), the first four requested now so
-    // their latency overlaps the output stage.
+    // the three 384-row blocks, tile t), the first QD requested now so their
+    // latency overlaps the output stage; its fold terms c1q/c2q go to the
+    // fold-term region (free: every wave has passed the chunk loop's last
+    // barrier, so no epilogue reads c1/c2 any more).
     const i32x4 *wqp = (const i32x4 *)g.wq + (size_t)wave * KS2 * NT2 * 64 + lane;
     auto wq_frag = [&](int kg, int t) {
         const int p = kg / KS1, k = kg - p * KS1;
         return wqp[(size_t)p * (HD * HD / 8) + (size_t)(k / KS2) * W2C + ((k % KS2) * NT2 + t) * 64];
     };
-    i32x4 wqf[KS2][NT2];
+    i32x4 wqf[QD][NT2];
     if constexpr (QKVN) {
+        const __amdgpu_buffer_rsrc_t rQ1 = buf_rsrc(g.c1q, 3 * HD * 4), rQ2 = buf_rsrc(g.c2q, 3 * HD * 4);
+        constexpr int NCB = (3 * HD * 4 + 1023) / 1024;
+        for (int b = wave; b < 2 * NCB; b += NW) {
+            const int which = b >= NCB, kb = b - which * NCB;
+            dma16(which ? rQ2 : rQ1, lds0 + C_OFF + (uint32_t)which * (I_MAX * 4) + (uint32_t)kb * 1024,
+                  (uint32_t)lane * 16, (uint32_t)kb * 1024);
+        }
 #pragma unroll
-        for (int ks = 0; ks < KS2; ++ks)
+        for (int ks = 0; ks < QD; ++ks)
 #pragma unroll
             for (int t = 0; t < NT2; ++t) wqf[ks][t] = wq_frag(ks, t);
     }
@@ -447,56 +464,70 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             *(f16x4 *)(otile + off) = o;
         }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    {
-        const __amdgpu_buffer_rsrc_t rO = buf_rsrc(g.out, (uint32_t)g.M * (HD * 2));
+    // (with QKVN also the fold-term transfers)
+    if constexpr (QKVN) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Rows [BM, 384] of an LDS tile in the swizzled layout to rows of `rs`
+    // (row pitch `pitch` bytes, column offset `col` bytes), 16-byte coalesced
+    // stores; rows past M are dropped by the buffer bounds.
+    auto store_tile = [&](const uint8_t *tile, __amdgpu_buffer_rsrc_t rs, int pitch, int col) {
         constexpr int UPR = HD * 2 / 16;  // 16-byte units per row
         for (int u = (int)threadIdx.x; u < BM * UPR; u += 64 * NW) {
             const int r = u / UPR, cu = u - r * UPR;
-            const i32x4 v = *(const i32x4 *)(otile + (cu >> 3) * BM * ROWB + r * ROWB + (((cu & 7) ^ (r & 7)) << 4));
-            __builtin_amdgcn_raw_buffer_store_b128(v, rO, (uint32_t)((m0 + r) * HD * 2 + cu * 16), 0, 0);
+            const i32x4 v = *(const i32x4 *)(tile + (cu >> 3) * BM * ROWB + r * ROWB + (((cu & 7) ^ (r & 7)) << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, (uint32_t)((m0 + r) * pitch + col + cu * 16), 0, 0);
         }
-    }
-    if (g.stats_out || QKVN)
+    };
+    store_tile(otile, buf_rsrc(g.out, (uint32_t)g.M * (HD * 2)), HD * 2, 0);
+    auto out_stats = [&] {
         tile_stats(otile, lane, [&](int r, f32x2 st) {
             if (g.stats_out && m0 + r < g.M) g.stats_out[m0 + r] = st;
             if (QKVN) lst[r] = st;  // every wave has read y's statistics (barrier above)
         });
-    if constexpr (QKVN) {
+    };
+    if constexpr (!QKVN) {
+        if (g.stats_out) out_stats();
+    } else {
         // The next layer's QKV projection of the output tile (the QKV GEMM's
         // LN_IN form: same K order, same fold arithmetic), 384 columns per
         // pass.  The three passes are one stream of 3·KS1 k-steps for the Wq
-        // ring (four k-steps ahead, its first fragments requested before the
-        // output epilogue), so a pass's epilogue overlaps the next pass's
-        // loads; each lane stores its 4·NT2 consecutive columns per token.
+        // ring (QD k-steps ahead), so a pass's epilogue overlaps the next
+        // pass's loads.  The output tile's statistics, which only the
+        // epilogues need, are computed beside the first pass's products.  A
+        // pass's binary16 results are staged in the token tile (free after
+        // the output epilogue) and stored as whole rows.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const __amdgpu_buffer_rsrc_t rQ = buf_rsrc(g.qkv, (uint32_t)g.M * (3 * HD * 2));
-        const int n0 = wave * 16 * NT2 + (lane >> 4) * 4 * NT2;
+        uint8_t *const stile = lds;
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
-            f32x4 kc1[NT2], kc2[NT2];
-#pragma unroll
-            for (int t = 0; t < NT2; ++t) {
-                kc1[t] = *(const f32x4 *)(g.c1q + p * HD + n0 + 4 * t);
-                kc2[t] = *(const f32x4 *)(g.c2q + p * HD + n0 + 4 * t);
-            }
             f32x4 accq[NT2][MT];
+            i32x4 afq[2][MT];
+            load_tile_frags(afq[0], otile, 0);
 #pragma unroll
             for (int k = 0; k < KS1; ++k) {
                 const int kg = p * KS1 + k;  // position in the stream
-                const uint8_t *ab = otile + (k >> 1) * BM * ROWB + fo[k & 1];
-                i32x4 af[MT];
-#pragma unroll
-                for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(ab + t * 16 * ROWB);
+                if (k + 1 < KS1) load_tile_frags(afq[(k + 1) & 1], otile, k + 1);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = 0; t < NT2; ++t) {
 #pragma unroll
                     for (int tm = 0; tm < MT; ++tm)
                         accq[t][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, wqf[kg % KS2][t]), __builtin_bit_cast(f16x8, af[tm]),
+                            __builtin_bit_cast(f16x8, wqf[kg % QD][t]), __builtin_bit_cast(f16x8, afq[k & 1][tm]),
                             k == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : accq[t][tm], 0, 0, 0);
-                    if (kg + KS2 < 3 * KS1) wqf[kg % KS2][t] = wq_frag(kg + KS2, t);
+                    if (kg + QD < 3 * KS1) wqf[kg % QD][t] = wq_frag(kg + QD, t);
                 }
+                if (p == 0 && k == 1) out_stats();
+            }
+            // The statistics (pass 0) are visible, and every wave has read
+            // the previous pass's staged rows.
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            f32x4 kc1[NT2], kc2[NT2];
+#pragma unroll
+            for (int t = 0; t < NT2; ++t) {
+                kc1[t] = *(const f32x4 *)(lc1 + p * HD + n0 + 4 * t);
+                kc2[t] = *(const f32x4 *)(lc2 + p * HD + n0 + 4 * t);
             }
 #pragma unroll
             for (int tm = 0; tm < MT; ++tm) {
@@ -508,11 +539,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     f16x4 o;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) o[i] = to_f16(x[i]);
-                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rQ,
-                                                          (uint32_t)(((m0 + r) * 3 * HD + p * HD + n0 + 4 * t) * 2), 0,
-                                                          0);
+                    const int n = n0 + 4 * t;
+                    *(f16x4 *)(stile + (n >> 6) * BM * ROWB + r * ROWB + ((((n & 63) >> 3) ^ (lane & 7)) << 4) +
+                               (n & 7) * 2) = o;
                 }
             }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            store_tile(stile, rQ, 3 * HD * 2, p * HD * 2);
         }
     }
     }
