@@ -160,6 +160,9 @@ __host__ __device__ inline void mlp_w2_unit(long u, int K, int &row, int &col) {
 }
 // out = the fragment-ordered copy of B [N, K]: kind 1 (fc1, K % 32 == 0,
 // N % (16·MLP_NT1) == 0) or kind 2 (N % 384 == 0, K % 128 == 0).
+// Compute units of the current device (queried once per process; 0 when
+// the query fails).
+int cu_count();
 hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s);
 // Whether mlp() takes an M-row problem with intermediate width I, and
 // whether it can also write the next layer's Q/K/V for M rows (32-bit

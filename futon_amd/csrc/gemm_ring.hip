@@ -325,13 +325,8 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
 
 template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        hipDeviceProp_t p;
-        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return hipErrorUnknown;
-        ncu = p.multiProcessorCount;
-    }
+    const int ncu = fh::cu_count();
+    if (ncu <= 0) return hipErrorUnknown;
     const int ntn = g.N / BN;
     const long ntiles = (long)((g.M + R::BM - 1) / R::BM) * ntn;
     // A multiple of 8 blocks (whole XCD groups); persistent: as many as the

@@ -561,17 +561,6 @@ __global__ void mlp_pack_kernel(int kind, const f16 *__restrict__ B, f16 *__rest
     *(f16x8 *)(out + u * 8) = *(const f16x8 *)(B + (size_t)row * K + col);
 }
 
-int cu_count() {
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        hipDeviceProp_t p;
-        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
-        ncu = p.multiProcessorCount;
-    }
-    return ncu;
-}
-
 template <int MT>
 hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
     const int grid = (g.M + 16 * MT - 1) / (16 * MT);
@@ -590,6 +579,17 @@ hipError_t launch_mlp(const MlpArgs &g, hipStream_t s) {
 }  // namespace
 
 namespace fh {
+
+int cu_count() {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+        ncu = p.multiProcessorCount;
+    }
+    return ncu;
+}
 
 hipError_t mlp_pack(int kind, const f16 *B, f16 *out, int N, int K, hipStream_t s) {
     if (N <= 0 || K <= 0 || !(kind == 1 ? N % (16 * NT1) == 0 && K % 32 == 0 : kind == 2 && N % HD == 0 && K % CH == 0))
@@ -612,7 +612,7 @@ hipError_t mlp(const MlpArgs &g, hipStream_t s) {
         return hipErrorInvalidValue;
     if (g.attn ? !g.wo || !g.ya || !g.stats_a || !g.ga || !g.ba || g.stats : !g.y) return hipErrorInvalidValue;
     if (g.wq && (!g.attn || !g.c1q || !g.c2q || !g.qkv || !mlp_qkv_ok(g.M))) return hipErrorInvalidValue;
-    const int ncu = cu_count();
+    const int ncu = fh::cu_count();
     if (ncu <= 0) return hipErrorUnknown;
     // Tokens per block: the fewest 16-row tiles that cover M with one block
     // per CU (weights are re-read once per block, so fewer, larger blocks).
