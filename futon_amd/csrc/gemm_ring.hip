@@ -3,14 +3,17 @@
 // (native/kernel.go:26-43) with the same epilogues as gemm.hip (bias, GELU,
 // residual, the folded-LayerNorm modes).
 //
-// Layout and schedule (the default configuration, R2 below; the others are
-// tuning alternatives):
+// Layout and schedule (the default configurations, R2 and R5 below; the
+// others are tuning alternatives):
 // * Two persistent 4-wave blocks per CU, each looping over 128×128 output
-//   tiles (a wave owns 64×64); each of the 8 XCDs owns a contiguous range of
+//   tiles (a wave owns 64×64), or, for GEMMs whose 256×256 tiles cover every
+//   CU (the BERT-base-sized projections), one persistent 8-wave block per CU
+//   over 256×256 tiles (a wave owns 128×64), which halves the operand bytes
+//   streamed per MFMA.  Each of the 8 XCDs owns a contiguous range of
 //   tiles, so an A row panel is fetched into one XCD's L2 and reused there
 //   by all of that panel's column tiles.
-// * Operands stream into a 2-slot LDS ring (32 KB per 64-wide K slice per
-//   block) straight from global memory with buffer_load … lds (no VGPR
+// * Operands stream into a 2-slot LDS ring (32 or 64 KB per 64-wide K slice
+//   per block) straight from global memory with buffer_load … lds (no VGPR
 //   staging, no LDS store instructions).  The ring runs across tile
 //   boundaries: the next tile's first slice is in flight during the current
 //   tile's last slice and its epilogue, and while one block waits at its
@@ -38,22 +41,24 @@ using namespace fh_epi;
 using fh_dma::buf_rsrc;
 using fh_dma::dma16;
 
-constexpr int ROWB = 128;  // bytes of K per slice row (64 f16)
-
 // Ring configuration: BM×BN output tile, WM×WN waves, SLOTS ring slots;
 // PERSIST: one block per CU looping over tiles (else one block per tile,
-// the hardware scheduling them as CUs free up).
-template <int BM_, int BN_, int WM_, int WN_, int SLOTS_, bool PERSIST_>
+// the hardware scheduling them as CUs free up); ROWB: bytes of K per slice
+// row (128: 64-wide K slices; 64: 32-wide, for deeper rings).
+template <int BM_, int BN_, int WM_, int WN_, int SLOTS_, bool PERSIST_, int ROWB_ = 128>
 struct RCfg {
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SLOTS = SLOTS_;
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SLOTS = SLOTS_, ROWB = ROWB_;
     static constexpr bool PERSIST = PERSIST_;
+    static constexpr int RPB = 1024 / ROWB;                // slot rows per 1-KB DMA block
+    static constexpr int KS = ROWB / 64;                   // 32-wide MFMA k-steps per slice
     static constexpr int NT = 64 * WM * WN;                // threads
     static constexpr int MT = BM / WM / 16;                // token tiles per wave
     static constexpr int NTL = BN / WN / 16;               // feature tiles per wave (the 64-row packing block)
     static constexpr int STAGE = (BM + BN) * ROWB;         // bytes per ring slot
-    static constexpr int DPW = (BM + BN) / 8 / (WM * WN);  // 1-KB DMA blocks per wave per slice
+    static constexpr int DPW = (BM + BN) / RPB / (WM * WN);  // 1-KB DMA blocks per wave per slice
     static constexpr int BPC = 163840 / (SLOTS * STAGE);   // blocks per CU the LDS allows
-    static_assert(NTL == 4 && DPW * 8 * WM * WN == BM + BN && BM % 8 == 0 && SLOTS >= 2 && BPC >= 1,
+    static_assert(NTL == 4 && DPW * RPB * WM * WN == BM + BN && BM % RPB == 0 && SLOTS >= 2 && BPC >= 1 &&
+                      (ROWB == 128 || ROWB == 64),
                   "ring tile shape");
 };
 constexpr int BN = 128;     // every configuration's column tile (the packing unit × 2)
@@ -66,8 +71,8 @@ template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void ring_kernel(GemmArgs g, int ntn,
                                                                                               int per_xcd) {
     constexpr int BM = R::BM, WN = R::WN, SLOTS = R::SLOTS;
-    constexpr int MT = R::MT, NTL = R::NTL, STAGE = R::STAGE, DPW = R::DPW;
-    static_assert(R::BN == BN, "column tile");
+    constexpr int MT = R::MT, NTL = R::NTL, STAGE = R::STAGE, DPW = R::DPW, BN = R::BN;
+    constexpr int ROWB = R::ROWB, RPB = R::RPB, KS = R::KS;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[SLOTS * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -80,7 +85,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     const int nbx = gridDim.x >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
     const int t0 = xcd * per_xcd + j, tend = min(ntiles, (xcd + 1) * per_xcd);
     const int ntile = t0 < tend ? (tend - t0 + nbx - 1) / nbx : 0;
-    const int nk = g.K / 64;
+    const int nk = g.K / (ROWB / 2);
     const int nsl = ntile * nk;  // slices this block multiplies
     if (nsl == 0) return;
 
@@ -89,15 +94,19 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     const __amdgpu_buffer_rsrc_t rB = buf_rsrc(g.B, (uint32_t)g.N * ldb_b);
     const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
 
-    // DMA block b of a slot holds slot rows 8b..8b+7 (rows < BM: A, else B);
-    // lane l writes physical chunk l%8 of row 8b + l/8, i.e. logical chunk
-    // (l%8) ^ (l/8).
-    const uint32_t lrow = lane >> 3, lchunk = ((lane & 7) ^ (lane >> 3)) * 16;
+    // DMA block b of a slot holds slot rows RPB·b .. RPB·b + RPB − 1 (rows
+    // < BM: A, else B).  128-byte rows: lane l writes physical chunk l%8 of
+    // row 8b + l/8, i.e. logical chunk (l%8) ^ (l/8).  64-byte rows: lane l
+    // writes physical chunk l%4 of row 16b + l/4, logical chunk
+    // (l%4) ^ ((l/16)%4).  Either way the 16 rows × one logical chunk that a
+    // fragment read takes land on 16 distinct 16-byte bank groups.
+    const uint32_t lrow = ROWB == 128 ? lane >> 3 : lane >> 2;
+    const uint32_t lchunk = (ROWB == 128 ? (lane & 7) ^ (lane >> 3) : (lane & 3) ^ ((lane >> 4) & 3)) * 16;
     // Per DMA block of this wave (wave-uniform, fixed for the kernel): operand
     // and row offset inside the tile's operand rows.
     bool isA[DPW];
 #pragma unroll
-    for (int i = 0; i < DPW; ++i) isA[i] = (wave * DPW + i) * 8 < BM;
+    for (int i = 0; i < DPW; ++i) isA[i] = (wave * DPW + i) * RPB < BM;
     // Issues the next slice of this block's sequence (past the end: the last
     // slice again, into a slot nobody reads) into the next slot.  Slices are
     // issued in order, so the slice's tile and K position advance by
@@ -130,17 +139,20 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
         for (int i = 0; i < DPW; ++i) {
             const uint32_t b = (uint32_t)(wave * DPW + i);
             const uint32_t dst = slot + b * 1024;
-            const uint32_t voff = isA[i] ? offA + b * 8 * lda_b : offB + b * 8 * ldb_b;
+            const uint32_t voff = isA[i] ? offA + b * RPB * lda_b : offB + b * RPB * ldb_b;
             if (isA[i]) dma16(rA, dst, voff, soff);
             else dma16(rB, dst, voff, soff);
         }
     };
 
     // Fragment offsets inside a slot: row r = base + lane%16 (base a multiple
-    // of 16), logical chunk lane/16 + 4·ks at physical chunk ^ (lane%8).
-    int fo[2];
+    // of 16), logical chunk lane/16 + 4·ks at physical chunk ^ (lane%8)
+    // (128-byte rows) or ^ ((lane%16)/4) (64-byte rows).
+    int fo[KS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) fo[ks] = (lane & 15) * ROWB + ((((lane >> 4) + 4 * ks) ^ (lane & 7)) << 4);
+    for (int ks = 0; ks < KS; ++ks)
+        fo[ks] = (lane & 15) * ROWB +
+                 ((ROWB == 128 ? ((lane >> 4) + 4 * ks) ^ (lane & 7) : (lane >> 4) ^ ((lane >> 2) & 3)) << 4);
     const int abase = wm * MT * 16 * ROWB, bbase = BM * ROWB + wn * NTL * 16 * ROWB;
 
     f32x4 acc[NTL][MT];
@@ -155,7 +167,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     auto compute = [&](int slot) {
         const uint8_t *base = ring + slot * STAGE;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             i32x4 af[MT], bf[NTL];
 #pragma unroll
             for (int t = 0; t < MT; ++t) af[t] = *(const i32x4 *)(base + abase + t * 16 * ROWB + fo[ks]);
@@ -181,6 +193,10 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     constexpr int ESZ = OUT_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t rC = buf_rsrc(g.C, (uint32_t)g.M * (uint32_t)g.ldc * ESZ);
     f32x4 k1[4], k2[4], kb[4], kg[4], kt[4];
+    // With eight token tiles a wave the binary16 residual does not fit in
+    // registers beside the last slice's operands: epi_store loads it instead
+    // (its wait then also covers the next slice's DMA, issued before).
+    constexpr bool LATE_RES = RES == 2 && MT > 4;
     f16x8 rh[MT][2];
     f32x2 sti[MT];  // (mean, rstd) of the row: A's (LN_IN) or the residual's (RES_LN)
     auto tile_of = [&](int ti, int &m0, int &nt) {
@@ -210,7 +226,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
 #pragma unroll
         for (int tm = 0; tm < MT; ++tm) {
             const int rr = min(m0 + (wm * MT + tm) * 16 + (lane & 15), g.M - 1);
-            if (RES == 2) {
+            if (RES == 2 && !LATE_RES) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) rh[tm][h] = *(const f16x8 *)(g.resid_h + (size_t)rr * g.ldr + cb + h * 32);
             }
@@ -223,6 +239,16 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
         const int cb = nt * BN + wn * NTL * 16 + (lane >> 4) * 8;
         // An f32 residual (too many registers to hold across the last slice)
         // is loaded here, still ahead of the stores.
+        // (late residual: two token tiles ahead of their use)
+        auto load_rh = [&](int tm) {
+            const int rr = min(m0 + (wm * MT + tm) * 16 + (lane & 15), g.M - 1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) rh[tm][h] = *(const f16x8 *)(g.resid_h + (size_t)rr * g.ldr + cb + h * 32);
+        };
+        if (LATE_RES) {
+            load_rh(0);
+            load_rh(1);
+        }
         f32x4 rf[MT][4];
         if (RES == 1) {
 #pragma unroll
@@ -235,6 +261,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
         }
 #pragma unroll
         for (int tm = 0; tm < MT; ++tm) {
+            if (LATE_RES && tm + 2 < MT) load_rh(tm + 2);
             const uint32_t row = (uint32_t)(m0 + (wm * MT + tm) * 16 + (lane & 15));
             const f32x2 rs = LNM != fh::LN_NONE ? sti[tm] : (f32x2){0.f, 0.f};
 #pragma unroll
@@ -327,7 +354,8 @@ template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     const int ncu = fh::cu_count();
     if (ncu <= 0) return hipErrorUnknown;
-    const int ntn = g.N / BN;
+    if (g.N % R::BN) return hipErrorInvalidValue;
+    const int ntn = g.N / R::BN;
     const long ntiles = (long)((g.M + R::BM - 1) / R::BM) * ntn;
     // A multiple of 8 blocks (whole XCD groups); persistent: as many as the
     // CUs hold at once.
@@ -355,33 +383,50 @@ hipError_t launch_ring_r(const GemmArgs &g, hipStream_t s) {
 }
 
 // Configurations (measured on the 18k-token bge-small projections, op level:
-// R0 30.2 µs for QKV, R1 27.8, R2 25.0, R3 32.9, R4 32.7).  The default, R2,
-// runs two persistent 4-wave blocks per CU: while one block waits at its
-// barrier or runs its epilogue, the other keeps the matrix cores busy.
+// R0 30.2 µs for QKV, R1 27.8, R2 25.0, R3 32.9, R4 32.7).  R2 runs two
+// persistent 4-wave blocks per CU: while one block waits at its barrier or
+// runs its epilogue, the other keeps the matrix cores busy.  R5's 256×256
+// tiles need half the operand bytes per MFMA of R2's 128×128 (the slices
+// stream from L2 at ~16 B/clk per CU on the 65k-token BERT-base projections:
+// R5 is 12–14% faster there).  R6 measured slower than R5 (same stream rate,
+// twice the barriers).
 using R0 = RCfg<256, 128, 4, 2, 3, true>;   // 8 waves, 3 slots, one persistent block per CU
 using R1 = RCfg<128, 128, 2, 2, 2, false>;  // 4 waves, 2 slots, one block per tile (two per CU)
 using R2 = RCfg<128, 128, 2, 2, 2, true>;   // R1's blocks, persistent, two per CU
 using R3 = RCfg<128, 128, 4, 2, 3, true>;   // 8 waves of 32×64, 3 slots, persistent
 using R4 = RCfg<256, 128, 4, 2, 3, false>;  // R0's tile, one block per tile
+using R5 = RCfg<256, 256, 2, 4, 2, true>;   // 8 waves of 128×64, 2 slots, one persistent block per CU
+using R6 = RCfg<256, 256, 2, 4, 5, true, 64>;  // R5's tile, 5 slots of 32-wide K slices
 
-// FUTON_RING_CFG=0..4 picks a configuration (tuning knob; default 2).
+// FUTON_RING_CFG=0..6 forces a configuration (tuning knob); unset: R5 where
+// its tiles fit (N a multiple of 256, no f32 residual) and fill every CU at
+// least once, else R2.
 int ring_cfg() {
     static const int v = [] {
         const char *e = getenv("FUTON_RING_CFG");
-        const int c = e ? atoi(e) : 2;
-        return c >= 0 && c <= 4 ? c : 2;
+        const int c = e ? atoi(e) : -1;
+        return c >= 0 && c <= 6 ? c : -1;
     }();
     return v;
 }
 
 template <int ACT, bool OUT_F32, int LNM>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+    const bool fit256 = g.N % R5::BN == 0 && !g.resid;
     switch (ring_cfg()) {
     case 0: return launch_ring_r<R0, ACT, OUT_F32, LNM>(g, s);
     case 1: return launch_ring_r<R1, ACT, OUT_F32, LNM>(g, s);
+    case 2: return launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
     case 3: return launch_ring_r<R3, ACT, OUT_F32, LNM>(g, s);
     case 4: return launch_ring_r<R4, ACT, OUT_F32, LNM>(g, s);
-    default: return launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
+    case 5: return fit256 ? launch_ring_r<R5, ACT, OUT_F32, LNM>(g, s) : launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
+    case 6:
+        return fit256 && LNM != fh::RES_LN ? launch_ring_r<R6, ACT, OUT_F32, LNM>(g, s)
+                                           : launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
+    default:
+        if (fit256 && (long)((g.M + R5::BM - 1) / R5::BM) * (g.N / R5::BN) >= fh::cu_count())
+            return launch_ring_r<R5, ACT, OUT_F32, LNM>(g, s);
+        return launch_ring_r<R2, ACT, OUT_F32, LNM>(g, s);
     }
 }
 

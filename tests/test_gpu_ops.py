@@ -114,12 +114,15 @@ def gemm_ring(A, Bp, bias=None, resid=None, act=0, out_f32=True):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 64), (77, 128, 64), (300, 384, 384), (513, 1152, 384),
-                                   (1030, 1536, 384), (257, 384, 1536), (2049, 768, 768), (18048, 384, 384)])
+                                   (1030, 1536, 384), (257, 384, 1536), (2049, 768, 768), (18048, 384, 384),
+                                   (8269, 2048, 128)])
 def test_gemm_ring_equals_tiled(M, N, K):
     """The persistent LDS-ring GEMM on packed weights returns fh_op_gemm's
     bits on the unpacked weights (same K order, same epilogue arithmetic),
     for f32 and binary16 outputs with bias, GELU and f32 / binary16
-    residuals; ragged M exercises the zero rows past the end."""
+    residuals; ragged M exercises the zero rows past the end.  8269×2048
+    has enough 256×256 tiles to fill a 256-CU part, so it takes that ring
+    layout (an f32 residual stays on 128×128)."""
     rng = np.random.default_rng(M * 5 + N + K)
     a = rng.standard_normal((M, K)).astype(np.float16)
     b = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
@@ -190,7 +193,7 @@ def test_row_stats_matches_float64(M, H):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 384, 384), (1030, 1536, 384), (257, 384, 768), (600, 1152, 384),
-                                   (12288, 1152, 384), (12288, 384, 1536)])
+                                   (12288, 1152, 384), (12288, 384, 1536), (8269, 2048, 256)])
 def test_gemm_ln_modes(M, N, K):
     """The folded-LayerNorm GEMM forms: LN_IN (C = act(rstd·(A·Bᵀ − mean·c1)
     + c2) with A's row statistics) and RES_LN (the residual's LayerNorm
