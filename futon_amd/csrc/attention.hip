@@ -525,8 +525,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
     const float sl2 = a.scale_log2e;
 
     // One query tile against key block `buf` (kvalid valid keys from its
-    // first).
-    auto qtile = [&](int qt, int buf, int kvalid) {
+    // first).  MASK: the block has fewer than BK valid keys (only the last
+    // can); a separate copy, so that full blocks carry no masking selects.
+    auto qtile = [&](int qt, int buf, int kvalid, auto mask_t) {
+        constexpr bool MASK = decltype(mask_t)::value;
         f32x4 s[NKT];
         float mx = -INFINITY;
 #pragma unroll
@@ -537,7 +539,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
                 const f16x8 kf = *(const f16x8 *)&Ks[buf][(kt * 16 + (lane & 15)) * KS + dk * 32 + (lane >> 4) * 8];
                 s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qt][dk], s[kt], 0, 0, 0);
             }
-            if (kvalid < BK) {  // the last key block: keys past the sequence
+            if constexpr (MASK) {  // the last key block: keys past the sequence
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (kt * 16 + (lane >> 4) * 4 + i >= kvalid) s[kt][i] = -INFINITY;
@@ -584,9 +586,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
         const int kb0 = kb * BK, buf = kb & 1;
         const bool more = kb + 1 < nkb;
         if (more) load_kv(kb0 + BK);  // in flight while this block is multiplied
+        if (L - kb0 >= BK) {
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-            if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, L - kb0);  // wave-uniform
+            for (int qt = 0; qt < QT; ++qt)
+                if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, BK, std::false_type{});  // wave-uniform
+        } else {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+                if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, L - kb0, std::true_type{});
+        }
         // The other buffer was last read before the previous barrier.
         if (more) store_kv(buf ^ 1, kb0 + BK);
         __syncthreads();

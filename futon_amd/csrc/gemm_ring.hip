@@ -69,7 +69,7 @@ constexpr int BM_MAX = 256;
 // vector memory instructions it issues is a constant the ring's waits use.
 template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void ring_kernel(GemmArgs g, int ntn,
-                                                                                              int per_xcd) {
+                                                                                              int per_part, int cg) {
     constexpr int BM = R::BM, WN = R::WN, SLOTS = R::SLOTS;
     constexpr int MT = R::MT, NTL = R::NTL, STAGE = R::STAGE, DPW = R::DPW, BN = R::BN;
     constexpr int ROWB = R::ROWB, RPB = R::RPB, KS = R::KS;
@@ -79,11 +79,15 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
-    // This block's tiles: XCD x (= block id mod 8) owns tiles
-    // [x·per_xcd, (x+1)·per_xcd); its blocks take them round-robin.
-    const int ntiles = ((g.M + BM - 1) / BM) * ntn;
+    // This block's tiles: the column tiles are split into cg groups of
+    // cols = ntn / cg, and XCD x (= block id mod 8) takes column group x % cg.
+    // The group's tiles, numbered row-major (u = row·cols + column), are
+    // split among its 8 / cg XCDs: XCD x owns [p·per_part, (p+1)·per_part)
+    // with p = x / cg, and its blocks take them round-robin.
     const int nbx = gridDim.x >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
-    const int t0 = xcd * per_xcd + j, tend = min(ntiles, (xcd + 1) * per_xcd);
+    const int cols = ntn / cg, col0 = (xcd % cg) * cols, part = xcd / cg;
+    const int ntiles = ((g.M + BM - 1) / BM) * cols;
+    const int t0 = part * per_part + j, tend = min(ntiles, (part + 1) * per_part);
     const int ntile = t0 < tend ? (tend - t0 + nbx - 1) / nbx : 0;
     const int nk = g.K / (ROWB / 2);
     const int nsl = ntile * nk;  // slices this block multiplies
@@ -114,11 +118,11 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     // that would delay the waves' matrix instructions every slice.
     int is_kk = 0, is_left = nsl, is_slot = 0, is_mt, is_nt;
     {
-        is_mt = t0 / ntn;
-        is_nt = t0 - is_mt * ntn;
+        is_mt = t0 / cols;
+        is_nt = t0 - is_mt * cols;
     }
     auto issue = [&] {
-        const int kk = is_kk, mt = is_mt, nt = is_nt;
+        const int kk = is_kk, mt = is_mt, nt = col0 + is_nt;
         const uint32_t slot = ring0 + (uint32_t)is_slot * STAGE;
         is_slot = is_slot + 1 == SLOTS ? 0 : is_slot + 1;
         if (is_left > 1) {  // advance to the following slice (the last one is repeated)
@@ -126,8 +130,8 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
             if (++is_kk == nk) {
                 is_kk = 0;
                 is_nt += nbx;  // the next tile of this block: t + nbx
-                while (is_nt >= ntn) {
-                    is_nt -= ntn;
+                while (is_nt >= cols) {
+                    is_nt -= cols;
                     ++is_mt;
                 }
             }
@@ -201,8 +205,8 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     f32x2 sti[MT];  // (mean, rstd) of the row: A's (LN_IN) or the residual's (RES_LN)
     auto tile_of = [&](int ti, int &m0, int &nt) {
         const int t = t0 + ti * nbx;
-        const int mt = t / ntn;
-        nt = t - mt * ntn;
+        const int mt = t / cols;
+        nt = col0 + t - mt * cols;
         m0 = mt * BM;
     };
     auto epi_load = [&](int ti) {
@@ -350,6 +354,20 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Column groups of the XCD tile split.  With 256-wide tiles and an even
+// number of them, two groups: each XCD then streams half of B (at BERT-base's
+// FFN1, 2.4 of 4.7 MB per XCD: fewer weight re-fetches into its 4 MB L2,
+// ~1.5% faster); otherwise one.  FUTON_RING_CG=1, 2 or 4 overrides (tuning
+// knob; ignored where it does not divide the column tiles).
+int ring_col_groups(int ntn, int bn) {
+    static const int v = [] {
+        const char *e = getenv("FUTON_RING_CG");
+        return e ? atoi(e) : 0;
+    }();
+    const int c = v == 1 || v == 2 || v == 4 ? v : bn == 256 ? 2 : 1;
+    return ntn % c == 0 ? c : 1;
+}
+
 template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     const int ncu = fh::cu_count();
@@ -361,8 +379,10 @@ hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     // CUs hold at once.
     const long all = (ntiles + 7) / 8 * 8;
     const int grid = (int)(R::PERSIST ? std::min<long>((long)(ncu / 8) * 8 * R::BPC, all) : all);
-    const int per_xcd = (int)((ntiles + 7) / 8);
-    hipLaunchKernelGGL((ring_kernel<R, ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(R::NT), 0, s, g, ntn, per_xcd);
+    const int cg = ring_col_groups(ntn, R::BN);
+    const int per_part = (int)((ntiles / cg + 8 / cg - 1) / (8 / cg));
+    hipLaunchKernelGGL((ring_kernel<R, ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(R::NT), 0, s, g, ntn, per_part,
+                       cg);
     return hipGetLastError();
 }
 
