@@ -1195,7 +1195,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     m->lnfold = !q8 && H % 64 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16) &&
                 !(fold_env && fold_env[0] == '0');
     // The folded binary16 projections run on the persistent ring GEMM when
-    // their shape fits it (N % 128, K % 64; not the SwiGLU pair);
+    // their shape fits it (N % 128, K % 64; the SwiGLU pair too);
     // FUTON_GEMM_RING=0 keeps them on the tiled GEMM (diagnostics).
     const char *ring_env = getenv("FUTON_GEMM_RING");
     const bool ring_on = m->lnfold && !(ring_env && ring_env[0] == '0');
@@ -1261,7 +1261,7 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
                     (rc = upload(m, &L.ffn1_c2, c2.data(), c2.size() * 4)))
                     return bail(rc);
             }
-            if ((rc = upload_mat(m, L.ffn1, packed, 2 * I, H, q8))) return bail(rc);
+            if ((rc = upload_mat(m, L.ffn1, packed, 2 * I, H, q8, ring_fits(2 * I, H)))) return bail(rc);
         } else {
             if (m->lnfold) {
                 if ((rc = ld.vec_host(nm("mlp.fc1.bias"), I, bias, true))) return bail(rc);
@@ -1576,7 +1576,9 @@ extern "C" int32_t fh_route_flags(int32_t hidden, int32_t inter, int32_t swiglu,
     const DevMat q = mat(3 * H, H), o = mat(H, H), f1 = mat(swiglu ? 2 * I : I, H), f2 = mat(H, I);
     if (use_ring(q, args(M, 3 * H, H, H, 3 * H, false), fh::ACT_NONE, false, fh::LN_IN)) f |= FH_ROUTE_RING_QKV;
     if (use_ring(o, args(M, H, H, H, H, true), fh::ACT_NONE, false, fh::RES_LN)) f |= FH_ROUTE_RING_OUT;
-    if (!swiglu && use_ring(f1, args(M, I, H, H, I, false), fh::ACT_GELU, false, fh::LN_IN)) f |= FH_ROUTE_RING_FFN1;
+    if (swiglu ? use_ring(f1, args(M, 2 * I, H, H, I, false), fh::ACT_SWIGLU, false, fh::LN_IN)
+               : use_ring(f1, args(M, I, H, H, I, false), fh::ACT_GELU, false, fh::LN_IN))
+        f |= FH_ROUTE_RING_FFN1;
     if (use_ring(f2, args(M, H, I, I, H, true), fh::ACT_NONE, false, fh::RES_LN)) f |= FH_ROUTE_RING_FC2;
     if (!swiglu && fh::mlp_ok(1, H, I) && I % 128 == 0) {
         DevLayer L;

@@ -104,7 +104,8 @@ hipError_t gemm_f16(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int
 hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 // Persistent LDS-ring GEMM (gemm_ring.hip).  B must be packed with
 // ring_pack_row (rows permuted inside each 64-row block); gemm_ring_ok says
-// whether a problem fits it (binary16, N % 128 == 0, K % 64 == 0, no SwiGLU).
+// whether a problem fits it (binary16, N % 128 == 0, K % 64 == 0; SwiGLU
+// with binary16 output only).
 bool gemm_ring_ok(const GemmArgs &a, int act, bool out_f32, int ln);
 // Whether an M×N problem has enough rows for the ring to beat the tiled GEMM.
 bool gemm_ring_worth(int M, int N);

@@ -46,8 +46,9 @@ extern "C" int fh_op_gemm_ring(const void *A, const void *B_packed, const float 
                                int32_t resid_f16, void *C, int32_t M, int32_t N, int32_t K, int32_t act,
                                int32_t out_f32, void *stream) {
     if (!A || !B_packed || !C || M < 0 || N <= 0 || K <= 0) return FH_EINVAL;
-    if (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU) return FH_EINVAL;
+    if (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU && act != FH_OP_ACT_SWIGLU) return FH_EINVAL;
     if (resid && resid_f16 && (out_f32 || act != FH_OP_ACT_NONE)) return FH_EINVAL;
+    if (act == FH_OP_ACT_SWIGLU && (out_f32 || resid)) return FH_EINVAL;
     if (M == 0) return FH_OK;
     GemmArgs g{};
     g.A = A;
@@ -61,7 +62,7 @@ extern "C" int fh_op_gemm_ring(const void *A, const void *B_packed, const float 
     g.K = K;
     g.lda = K;
     g.ldb = K;
-    g.ldc = N;
+    g.ldc = act == FH_OP_ACT_SWIGLU ? N / 2 : N;
     g.ldr = N;
     const int a = act == FH_OP_ACT_NONE && !out_f32 && g.resid_h ? fh::ACT_RES16 : act;
     if (!fh::gemm_ring_ok(g, a, out_f32 != 0, fh::LN_NONE)) return FH_EINVAL;
@@ -87,9 +88,11 @@ extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const
     g.stats_in = (const f32x2 *)stats;
     int a;
     if (ln_mode == fh::LN_IN) {
-        if (!c1 || !c2 || (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU)) return FH_EINVAL;
+        if (!c1 || !c2 || act < FH_OP_ACT_NONE || act > FH_OP_ACT_SWIGLU) return FH_EINVAL;
+        if (act == FH_OP_ACT_SWIGLU && N % 128) return FH_EINVAL;
         g.c1 = c1;
         g.c2 = c2;
+        g.ldc = act == FH_OP_ACT_SWIGLU ? N / 2 : N;
         a = act;
     } else if (ln_mode == fh::RES_LN) {
         if (!resid_h || !ln_g || !ln_b || act != FH_OP_ACT_NONE) return FH_EINVAL;

@@ -62,6 +62,20 @@ struct RCfg {
                   "ring tile shape");
 };
 constexpr int BN = 128;     // every configuration's column tile (the packing unit × 2)
+
+// {x of lane l, y of lane l} → {x, y} of lanes 0..31 and 32..63 exchanged
+// between the halves: lanes < 32 get {x[l], x[l + 32]}, lanes ≥ 32
+// {y[l − 32], y[l]} (v_permlane32_swap).  Operands and results pass through
+// empty asm statements: this compiler can otherwise fold float arithmetic on
+// the two results as if both were the first.
+__device__ __forceinline__ f32x2 swap_halves(float x, float y) {
+    unsigned a = __builtin_bit_cast(unsigned, x), b = __builtin_bit_cast(unsigned, y);
+    asm volatile("" : "+v"(a), "+v"(b));
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    unsigned r0 = r[0], r1 = r[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    return (f32x2){__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
+}
 constexpr int BM_MAX = 256;
 
 // RES: no residual (0), f32 (1) or binary16 (2); BIAS: g.bias is set.  The
@@ -268,6 +282,35 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
             if (LATE_RES && tm + 2 < MT) load_rh(tm + 2);
             const uint32_t row = (uint32_t)(m0 + (wm * MT + tm) * 16 + (lane & 15));
             const f32x2 rs = LNM != fh::LN_NONE ? sti[tm] : (f32x2){0.f, 0.f};
+            if constexpr (ACT == fh::ACT_SWIGLU) {
+                // B holds up and gate rows interleaved in 16-row blocks, so
+                // this lane's rows are the up (lanes < 32) or the gate
+                // (lanes ≥ 32) rows of features f + 0..7 (q = 0, 1) and
+                // f + 16 + 0..7 (q = 2, 3), f = 8·(lane/16 % 2), of the
+                // 64-row block's 32 outputs, and lane l ^ 32 holds the other
+                // rows of the same features.  After the fold and bias (each
+                // lane its own columns' terms, as gemm.hip), a permlane32
+                // swap leaves every lane both operands of one feature set:
+                // lanes < 32 the first, lanes ≥ 32 the second.
+                f32x4 xs[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f32x4 x = acc[q][tm];
+                    if (LNM == fh::LN_IN) x = ln_fold_v(x, rs, k1[q], k2[q]);
+                    if (BIAS) x += kb[q];
+                    xs[q] = x;
+                }
+                f16x8 o;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const f32x2 ug = swap_halves(xs[i >> 2][i & 3], xs[2 + (i >> 2)][i & 3]);
+                    o[i] = to_f16(ug[0] * silu(ug[1]));
+                }
+                const int ocol = (cb & ~63) / 2 + (lane >> 5) * 16 + ((lane >> 4) & 1) * 8;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), rC,
+                                                       (row * (uint32_t)g.ldc + (uint32_t)ocol) * ESZ, 0, 0);
+                continue;
+            }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 f32x4 v[2];
@@ -308,7 +351,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
         }
     };
     // Vector memory instructions epi_store issues after its loads.
-    constexpr int NSTORE = MT * (OUT_F32 ? 4 : 2);
+    constexpr int NSTORE = ACT == fh::ACT_SWIGLU ? MT : MT * (OUT_F32 ? 4 : 2);
 
     // Ring: slice s lives in slot s % SLOTS; SLOTS−1 slices are in flight
     // while one is multiplied.  Before multiplying slice s this wave waits
@@ -476,7 +519,9 @@ bool gemm_ring_worth(int M, int N) {
 
 bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
     if (g.M <= 0 || g.N % BN != 0 || g.K % 64 != 0 || g.K <= 0) return false;
-    if (act != ACT_NONE && act != ACT_GELU && act != ACT_RES16) return false;
+    if (act != ACT_NONE && act != ACT_GELU && act != ACT_RES16 && act != ACT_SWIGLU) return false;
+    // SwiGLU: binary16 out, ldc ≥ N/2, no residual
+    if (act == ACT_SWIGLU && (out_f32 || g.resid || g.resid_h || ln == RES_LN || g.ldc < g.N / 2)) return false;
     if (g.lda % 8 || g.ldb % 8 || g.ldc % 8 || ((g.resid || g.resid_h) && g.ldr % 8)) return false;
     if (act == ACT_RES16 && (out_f32 || !g.resid_h)) return false;
     if (ln == LN_IN && (out_f32 || g.resid || g.resid_h)) return false;
@@ -494,10 +539,12 @@ hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, in
     if (ln == LN_IN) {
         if (act == ACT_NONE) return launch_ring<ACT_NONE, false, LN_IN>(a, s);
         if (act == ACT_GELU) return launch_ring<ACT_GELU, false, LN_IN>(a, s);
+        if (act == ACT_SWIGLU) return launch_ring<ACT_SWIGLU, false, LN_IN>(a, s);
         return hipErrorInvalidValue;
     }
     if (ln == RES_LN) return launch_ring<ACT_RES16, false, RES_LN>(a, s);
     if (act == ACT_RES16) return launch_ring<ACT_RES16, false, LN_NONE>(a, s);
+    if (act == ACT_SWIGLU) return launch_ring<ACT_SWIGLU, false, LN_NONE>(a, s);
     if (act == ACT_GELU)
         return out_f32 ? launch_ring<ACT_GELU, true, LN_NONE>(a, s) : launch_ring<ACT_GELU, false, LN_NONE>(a, s);
     return out_f32 ? launch_ring<ACT_NONE, true, LN_NONE>(a, s) : launch_ring<ACT_NONE, false, LN_NONE>(a, s);

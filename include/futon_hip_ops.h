@@ -37,8 +37,9 @@ int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, c
 
 /* The same contraction on the persistent LDS-ring kernel (binary16 only):
  * B_packed is B with its rows permuted by fh_op_ring_pack.  Requires
- * N % 128 == 0 and K % 64 == 0; act is NONE or GELU.  Gives the same bits
- * as fh_op_gemm on the unpacked B.
+ * N % 128 == 0 and K % 64 == 0; act is NONE, GELU or SWIGLU (SwiGLU:
+ * binary16 output [M, N/2], no residual).  Gives the same bits as
+ * fh_op_gemm on the unpacked B.
  * Replaces: Kernel.MatMulTF16 (native/kernel.go:26-43). */
 int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, const void *resid, int32_t resid_f16,
                     void *C, int32_t M, int32_t N, int32_t K, int32_t act, int32_t out_f32, void *stream);
@@ -47,7 +48,9 @@ int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, cons
  * tiled kernel (ring = 0, B as is) or the ring kernel (ring = 1, B packed);
  * stats holds [M] (mean, rstd) float pairs (fh_op_row_stats):
  *  ln_mode 1 (LN_IN):  C = act(rstd·(A·Bᵀ − mean·c1) + c2) with A's row
- *                      statistics; act NONE or GELU.
+ *                      statistics; act NONE or GELU, or SWIGLU (B, c1
+ *                      and c2 interleaved as for fh_op_gemm, N % 128 == 0,
+ *                      C [M, N/2]).
  *  ln_mode 2 (RES_LN): C = A·Bᵀ + bias + (resid_h − mean)·rstd·ln_g + ln_b
  *                      with resid_h's row statistics, rounded once.
  * C is binary16 [M, N].  These are the model's LayerNorm folds of

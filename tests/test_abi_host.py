@@ -225,6 +225,8 @@ def test_routing_falls_back_before_32bit_offsets_overflow():
     assert f_ok & R.FH_ROUTE_RING_FFN1 and not f_over & R.FH_ROUTE_RING_FFN1
     assert f_over & R.FH_ROUTE_RING_OUT  # the narrower outputs still fit
     assert not f_ok & R.FH_ROUTE_MLP  # the fused tail is built for hidden 384 only
-    # SwiGLU's interleaved FFN1 always runs tiled; H=32 (toy) is not folded
-    assert not L.fh_route_flags(768, 3072, 1, 65536) & R.FH_ROUTE_RING_FFN1
+    # SwiGLU's interleaved FFN1 (N = 2·I, C [M, I]) takes the ring too, to the same row limit;
+    # H=32 (toy) is not folded
+    assert L.fh_route_flags(768, 3072, 1, lim - 1) & R.FH_ROUTE_RING_FFN1
+    assert not L.fh_route_flags(768, 3072, 1, lim + 1) & R.FH_ROUTE_RING_FFN1
     assert L.fh_route_flags(32, 64, 0, 1 << 20) == 0

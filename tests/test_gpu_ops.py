@@ -445,6 +445,60 @@ def test_gemm_swiglu_interleave(M, I, K):
     np.testing.assert_allclose(got, ref, atol=3e-4 * math.sqrt(K), rtol=1e-4)
 
 
+def swiglu_pack(up, gate, bu=None, bg=None):
+    """fc1 and gate rows interleaved in 16-row blocks (the layout fh_op_gemm's
+    SwiGLU reads), with the biases in the same order."""
+    I, K = up.shape
+    packed = np.empty((2 * I, K), up.dtype)
+    pb = np.empty(2 * I, np.float32) if bu is not None else None
+    for r in range(2 * I):
+        blk, w = divmod(r, 32)
+        src, sb, sr = (up, bu, 16 * blk + w) if w < 16 else (gate, bg, 16 * blk + w - 16)
+        packed[r] = src[sr]
+        if pb is not None:
+            pb[r] = sb[sr]
+    return packed, pb
+
+
+@pytest.mark.parametrize("M,I,K", [(300, 256, 384), (77, 64, 128), (8269, 1024, 256)])
+def test_gemm_ring_swiglu_equals_tiled(M, I, K):
+    """SwiGLU on the ring kernel (up/gate rows of a feature meet across lane
+    halves through a permlane32 swap) returns the tiled kernel's binary16
+    bits, plain with bias and in the LN_IN fold; 8269 rows take the 256×256
+    ring layout on a 256-CU part."""
+    rng = np.random.default_rng(M + I + K)
+    a = (rng.standard_normal((M, K)) * 2 + 0.5).astype(np.float16)
+    up = (rng.standard_normal((I, K)) * 0.05).astype(np.float16)
+    gate = (rng.standard_normal((I, K)) * 0.05).astype(np.float16)
+    bu = rng.standard_normal(I).astype(np.float32)
+    bg = rng.standard_normal(I).astype(np.float32)
+    packed, pb = swiglu_pack(up, gate, bu, bg)
+    N = 2 * I
+    da, dw, dpb = dev(a), dev(packed), dev(pb)
+    wp = torch.empty_like(dw)
+    assert _lib().fh_op_ring_pack(ptr(dw), ptr(wp), N, K, None) == 0
+    want = gemm(0, da, dw, dpb, act=2, out_f32=False)
+    C = torch.empty((M, I), dtype=torch.float16, device="cuda")
+    assert _lib().fh_op_gemm_ring(ptr(da), ptr(wp), ptr(dpb), None, 0, ptr(C), M, N, K, 2, 0, None) == 0
+    sync()
+    got = C.cpu().numpy()
+    assert np.array_equal(got, want), np.abs(got.astype(np.float64) - want).max()
+    u = a.astype(np.float64) @ up.astype(np.float64).T + bu
+    g = a.astype(np.float64) @ gate.astype(np.float64).T + bg
+    ref = u * (g / (1.0 + np.exp(-g)))
+    np.testing.assert_allclose(got.astype(np.float64), ref, atol=3e-4 * math.sqrt(K) + 2e-2, rtol=2e-3)
+    # LN_IN fold: c1 = row sums of the stored weights, c2 per interleaved row
+    st = dev(np.stack(stats64(a, 1e-5), 1).astype(np.float32))
+    c1 = packed.astype(np.float64).sum(1).astype(np.float32)
+    c2 = rng.standard_normal(N).astype(np.float32)
+    dc1, dc2 = dev(c1), dev(c2)
+    outs = []
+    for ring, b in ((0, dw), (1, wp)):
+        C = torch.empty((M, I), dtype=torch.float16, device="cuda")
+        outs.append(gemm_ln(ring, 1, da, b, C, st, 2, dc1, dc2))
+    assert np.array_equal(outs[0], outs[1]), np.abs(outs[0].astype(np.float64) - outs[1]).max()
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4, 16), (7, 16, 48), (37, 96, 384), (300, 1152, 384), (65, 384, 1536),
                                    (9, 64, 768), (5, 32, 3072)])
 def test_q8_quantize_and_gemm_bit_exact(M, N, K):
