@@ -165,11 +165,13 @@ def test_gpu_matches_hf_bert_at_real_shapes(name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192), ("bert-base", 24)])
+@pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192), ("bert-base", 24),
+                                        ("nomic-bert", 4)])
 def test_ring_gemm_forward_equals_tiled(name, batch, monkeypatch):
     """The folded binary16 forward returns the same bits whether its
     projections run on the persistent ring GEMM (the default, at these
-    12k-13k token batches) or on the tiled GEMM (FUTON_GEMM_RING=0): same K
+    5k-13k token batches; BERT-base's QKV and FFN1 and nomic-bert's SwiGLU
+    FFN1 on 256×256 tiles) or on the tiled GEMM (FUTON_GEMM_RING=0): same K
     order, same LayerNorm statistics reduction, same epilogue arithmetic.
     The CLS-pooled last layer (bge-small) runs tiled in both."""
     w = synth.workload(name)
