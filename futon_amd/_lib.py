@@ -30,7 +30,7 @@ EXPORTED = (
     "fh_noalloc_scratch_bytes", "fh_profile_enable",
     "fh_profile_reset", "fh_profile_read", "fh_debug_cancel_after", "fh_checkpoints_per_call",
     "fh_strerror", "fh_last_error", "fh_model_device_bytes",
-    "fh_op_gemm", "fh_op_gemm_ring", "fh_op_gemm_ln", "fh_op_row_stats", "fh_op_ring_pack", "fh_op_mlp_pack", "fh_op_mlp", "fh_op_outproj_mlp", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
+    "fh_op_gemm", "fh_op_gemm_ring", "fh_op_gemm_ring_q8", "fh_op_gemm_ln", "fh_op_row_stats", "fh_op_ring_pack", "fh_op_mlp_pack", "fh_op_mlp", "fh_op_outproj_mlp", "fh_op_attention", "fh_op_layer_norm", "fh_op_quantize_rows", "fh_op_embed_ln",
     "fh_op_pool", "fh_route_flags",
     "fh_tokenizer_new", "fh_tokenizer_encode", "fh_tokenizer_vocab_size", "fh_tokenizer_free",
     "fh_pack_load", "fh_pack_config_load", "fh_pack_config", "fh_pack_model_id", "fh_pack_tensor_count",
@@ -111,6 +111,7 @@ def load():
     L.fh_model_device_bytes.argtypes = [vp]
     L.fh_op_gemm.argtypes = [i32, vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, vp]
     L.fh_op_gemm_ring.argtypes = [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, vp]
+    L.fh_op_gemm_ring_q8.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.fh_op_ring_pack.argtypes = [vp, vp, i32, i32, vp]
     L.fh_op_mlp_pack.argtypes = [i32, vp, vp, i32, i32, vp]
     L.fh_op_mlp.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_float, i32, i32, i32, vp]

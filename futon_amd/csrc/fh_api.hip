@@ -411,6 +411,12 @@ int upload_mat(fh_model *m, DevMat &d, const std::vector<float> &w, int n, int k
         for (int j = 0; j < n; j++) sc[(size_t)j] = quantize_row_q8(&codes[(size_t)j * k], &w[(size_t)j * k], k);
         int rc = upload(m, (int8_t **)&d.w, codes.data(), codes.size());
         if (rc) return rc;
+        if (ring) {  // the codes' rows in ring_pack_row order; scales stay by output column
+            std::vector<int8_t> pc(codes.size());
+            for (int r = 0; r < n; r++)
+                std::copy_n(&codes[(size_t)fh::ring_pack_row(r) * k], k, &pc[(size_t)r * k]);
+            if ((rc = upload(m, (int8_t **)&d.wr, pc.data(), pc.size()))) return rc;
+        }
         return upload(m, &d.scale, sc.data(), sc.size() * 4);
     }
     std::vector<uint16_t> h(w.size());
@@ -718,9 +724,11 @@ int gemm(fh_model *m, int cls, const DevMat &w, const void *A, int lda, const fl
     const double bytes = (double)M * w.k * (i8 ? 1 : 2) + (double)w.n * w.k * (i8 ? 1 : 2) +
                          (double)M * outn * (out_f32 ? 4 : 2) + (resid ? (double)M * outn * 4 : resid_h ? (double)M * outn * 2 : 0.0);
     Scope sc(m, cls, flops, bytes, s);
-    const bool ring = !i8 && use_ring(w, g, act, out_f32, fh::LN_NONE);
+    const bool ring = i8 ? w.wr && fh::gemm_ring_worth(M, w.n) && fh::gemm_ring_q8_ok(g, act, out_f32)
+                         : use_ring(w, g, act, out_f32, fh::LN_NONE);
     if (ring) g.B = w.wr;
-    LCHK(ring ? fh::gemm_ring(g, act, out_f32, s) : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
+    LCHK(ring ? (i8 ? fh::gemm_ring_q8(g, act, out_f32, s) : fh::gemm_ring(g, act, out_f32, s))
+              : i8 ? fh::gemm_i8(g, act, out_f32, s) : fh::gemm_f16(g, act, out_f32, s));
     return FH_OK;
 }
 
@@ -1197,9 +1205,14 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     // The folded binary16 projections run on the persistent ring GEMM when
     // their shape fits it (N % 128, K % 64; the SwiGLU pair too);
     // FUTON_GEMM_RING=0 keeps them on the tiled GEMM (diagnostics).
+    // The int8 projections of the Q8 path run on the ring GEMM's int8 form
+    // (N % 128, K % 128).
     const char *ring_env = getenv("FUTON_GEMM_RING");
-    const bool ring_on = m->lnfold && !(ring_env && ring_env[0] == '0');
-    auto ring_fits = [&](int n, int k) { return ring_on && n % 128 == 0 && k % 64 == 0; };
+    const bool ring_env_on = !(ring_env && ring_env[0] == '0');
+    const bool ring_on = m->lnfold && ring_env_on;
+    auto ring_fits = [&](int n, int k) {
+        return q8 ? ring_env_on && n % 128 == 0 && k % 128 == 0 : ring_on && n % 128 == 0 && k % 64 == 0;
+    };
     // The feed-forward block runs fused (fh::mlp) for hidden width 384 with
     // GELU; FUTON_MLP=0 keeps the two ring GEMMs (diagnostics).
     const char *mlp_env = getenv("FUTON_MLP");

@@ -107,6 +107,11 @@ hipError_t gemm_i8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 // whether a problem fits it (binary16, N % 128 == 0, K % 64 == 0; SwiGLU
 // with binary16 output only).
 bool gemm_ring_ok(const GemmArgs &a, int act, bool out_f32, int ln);
+// The int8 form of the ring GEMM (A, B int8 codes with a_scale/b_scale, B
+// rows in ring_pack_row order; f32 or binary16 output, an f32 residual with
+// f32 output; act NONE or GELU): the same bits as gemm_i8.  K % 128 == 0.
+bool gemm_ring_q8_ok(const GemmArgs &a, int act, bool out_f32);
+hipError_t gemm_ring_q8(const GemmArgs &a, int act, bool out_f32, hipStream_t s);
 // Whether an M×N problem has enough rows for the ring to beat the tiled GEMM.
 bool gemm_ring_worth(int M, int N);
 hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln = LN_NONE);

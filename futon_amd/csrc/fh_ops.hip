@@ -69,6 +69,31 @@ extern "C" int fh_op_gemm_ring(const void *A, const void *B_packed, const float 
     return code_of(fh::gemm_ring(g, act, out_f32 != 0, (hipStream_t)stream));
 }
 
+extern "C" int fh_op_gemm_ring_q8(const void *A, const void *B_packed, const float *a_scale, const float *b_scale,
+                                  const float *bias, const float *resid, float *C, int32_t M, int32_t N, int32_t K,
+                                  int32_t act, void *stream) {
+    if (!A || !B_packed || !a_scale || !b_scale || !C || M < 0 || N <= 0 || K <= 0) return FH_EINVAL;
+    if (act != FH_OP_ACT_NONE && act != FH_OP_ACT_GELU) return FH_EINVAL;
+    if (M == 0) return FH_OK;
+    GemmArgs g{};
+    g.A = A;
+    g.B = B_packed;
+    g.a_scale = a_scale;
+    g.b_scale = b_scale;
+    g.bias = bias;
+    g.resid = resid;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = K;
+    g.ldb = K;
+    g.ldc = N;
+    g.ldr = N;
+    if (!fh::gemm_ring_q8_ok(g, act, true)) return FH_EINVAL;
+    return code_of(fh::gemm_ring_q8(g, act, true, (hipStream_t)stream));
+}
+
 extern "C" int fh_op_gemm_ln(int32_t ring, int32_t ln_mode, const void *A, const void *B, const float *c1,
                              const float *c2, const float *bias, const void *resid_h, const void *stats,
                              const float *ln_g, const float *ln_b, void *C, int32_t M, int32_t N, int32_t K,

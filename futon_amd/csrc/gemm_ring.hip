@@ -81,13 +81,17 @@ constexpr int BM_MAX = 256;
 // RES: no residual (0), f32 (1) or binary16 (2); BIAS: g.bias is set.  The
 // epilogue is straight-line code for each combination, so the number of
 // vector memory instructions it issues is a constant the ring's waits use.
-template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+// I8: A and B are int8 codes (v_mfma_i32_16x16x64_i8, exact i32 sums; a
+// 128-byte slice row is 128 values), scaled in the epilogue by
+// a_scale[row]·b_scale[col] as gemm.hip's int8 kernel does.
+template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES, bool I8 = false>
 __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void ring_kernel(GemmArgs g, int ntn,
                                                                                               int per_part, int cg) {
     constexpr int BM = R::BM, WN = R::WN, SLOTS = R::SLOTS;
     constexpr int MT = R::MT, NTL = R::NTL, STAGE = R::STAGE, DPW = R::DPW, BN = R::BN;
     constexpr int ROWB = R::ROWB, RPB = R::RPB, KS = R::KS;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[SLOTS * STAGE];
+    static_assert(!I8 || (ACT != fh::ACT_SWIGLU && LNM == fh::LN_NONE && RES != 2), "int8 ring forms");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -103,11 +107,12 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     const int ntiles = ((g.M + BM - 1) / BM) * cols;
     const int t0 = part * per_part + j, tend = min(ntiles, (part + 1) * per_part);
     const int ntile = t0 < tend ? (tend - t0 + nbx - 1) / nbx : 0;
-    const int nk = g.K / (ROWB / 2);
+    const int nk = g.K / (I8 ? ROWB : ROWB / 2);
     const int nsl = ntile * nk;  // slices this block multiplies
     if (nsl == 0) return;
 
-    const uint32_t lda_b = (uint32_t)g.lda * 2, ldb_b = (uint32_t)g.ldb * 2;
+    constexpr uint32_t EB = I8 ? 1 : 2;  // operand bytes per value
+    const uint32_t lda_b = (uint32_t)g.lda * EB, ldb_b = (uint32_t)g.ldb * EB;
     const __amdgpu_buffer_rsrc_t rA = buf_rsrc(g.A, (uint32_t)g.M * lda_b);
     const __amdgpu_buffer_rsrc_t rB = buf_rsrc(g.B, (uint32_t)g.N * ldb_b);
     const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
@@ -173,12 +178,13 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
                  ((ROWB == 128 ? ((lane >> 4) + 4 * ks) ^ (lane & 7) : (lane >> 4) ^ ((lane >> 2) & 3)) << 4);
     const int abase = wm * MT * 16 * ROWB, bbase = BM * ROWB + wn * NTL * 16 * ROWB;
 
-    f32x4 acc[NTL][MT];
+    using AccT = std::conditional_t<I8, i32x4, f32x4>;
+    AccT acc[NTL][MT];
     auto clear = [&] {
 #pragma unroll
         for (int a = 0; a < NTL; ++a)
 #pragma unroll
-            for (int b = 0; b < MT; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < MT; ++b) acc[a][b] = AccT{};
     };
     clear();
 
@@ -194,9 +200,14 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
 #pragma unroll
             for (int tn = 0; tn < NTL; ++tn)
 #pragma unroll
-                for (int tm = 0; tm < MT; ++tm)
-                    acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        __builtin_bit_cast(f16x8, bf[tn]), __builtin_bit_cast(f16x8, af[tm]), acc[tn][tm], 0, 0, 0);
+                for (int tm = 0; tm < MT; ++tm) {
+                    if constexpr (I8)
+                        acc[tn][tm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[tn], af[tm], acc[tn][tm], 0, 0, 0);
+                    else
+                        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bf[tn]),
+                                                                             __builtin_bit_cast(f16x8, af[tm]),
+                                                                             acc[tn][tm], 0, 0, 0);
+                }
         }
     };
 
@@ -210,7 +221,8 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
     // This lane's 16 features: cb + 32·h + 4·half + {0..3}, q = 2·h + half.
     constexpr int ESZ = OUT_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t rC = buf_rsrc(g.C, (uint32_t)g.M * (uint32_t)g.ldc * ESZ);
-    f32x4 k1[4], k2[4], kb[4], kg[4], kt[4];
+    f32x4 k1[4], k2[4], kb[4], kg[4], kt[4], ksb[4];
+    float ksa[MT];  // int8 scales: b_scale of this lane's columns, a_scale of its rows
     // With eight token tiles a wave the binary16 residual does not fit in
     // registers beside the last slice's operands: epi_store loads it instead
     // (its wait then also covers the next slice's DMA, issued before).
@@ -235,6 +247,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
                 k2[q] = *(const f32x4 *)(g.c2 + col);
             }
             if (BIAS) kb[q] = *(const f32x4 *)(g.bias + col);
+            if (I8) ksb[q] = *(const f32x4 *)(g.b_scale + col);
             if (LNM == fh::RES_LN) {
                 kg[q] = *(const f32x4 *)(g.ln_g + col);
                 kt[q] = *(const f32x4 *)(g.ln_b + col);
@@ -249,6 +262,7 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
                 for (int h = 0; h < 2; ++h) rh[tm][h] = *(const f16x8 *)(g.resid_h + (size_t)rr * g.ldr + cb + h * 32);
             }
             if (LNM != fh::LN_NONE) sti[tm] = g.stats_in[rr];
+            if (I8) ksa[tm] = g.a_scale[rr];
         }
     };
     auto epi_store = [&](int ti) {
@@ -317,7 +331,20 @@ __global__ __launch_bounds__(R::NT) __attribute__((amdgpu_waves_per_eu(2))) void
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
                     const int q = 2 * h + half;
-                    f32x4 x = acc[q][tm];
+                    f32x4 x;
+                    if constexpr (I8) {
+                        // The scaled sum is rounded before the bias is added
+                        // (gemm.hip's int8 epilogue; the empty asm keeps the
+                        // compiler from fusing the two into one fma).
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float v = __fmul_rn((float)acc[q][tm][i], __fmul_rn(ksa[tm], ksb[q][i]));
+                            asm("" : "+v"(v));
+                            x[i] = v;
+                        }
+                    } else {
+                        x = acc[q][tm];
+                    }
                     if (LNM == fh::LN_IN) x = ln_fold_v(x, rs, k1[q], k2[q]);
                     if (BIAS) x += kb[q];
                     if (ACT == fh::ACT_GELU) {
@@ -411,7 +438,7 @@ int ring_col_groups(int ntn, int bn) {
     return ntn % c == 0 ? c : 1;
 }
 
-template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES>
+template <class R, int ACT, bool OUT_F32, int LNM, bool BIAS, int RES, bool I8 = false>
 hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     const int ncu = fh::cu_count();
     if (ncu <= 0) return hipErrorUnknown;
@@ -424,7 +451,7 @@ hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     const int grid = (int)(R::PERSIST ? std::min<long>((long)(ncu / 8) * 8 * R::BPC, all) : all);
     const int cg = ring_col_groups(ntn, R::BN);
     const int per_part = (int)((ntiles / cg + 8 / cg - 1) / (8 / cg));
-    hipLaunchKernelGGL((ring_kernel<R, ACT, OUT_F32, LNM, BIAS, RES>), dim3(grid), dim3(R::NT), 0, s, g, ntn, per_part,
+    hipLaunchKernelGGL((ring_kernel<R, ACT, OUT_F32, LNM, BIAS, RES, I8>), dim3(grid), dim3(R::NT), 0, s, g, ntn, per_part,
                        cg);
     return hipGetLastError();
 }
@@ -494,6 +521,29 @@ hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     }
 }
 
+// The int8 forms (no LayerNorm fold): f32 residual (f32 output) or none.
+template <class R, int ACT, bool OUT_F32>
+hipError_t launch_ring_q8_r(const GemmArgs &g, hipStream_t s) {
+    if constexpr (R::BN == 256 || !OUT_F32) {  // no f32 residual here (launch_ring_q8, gemm_ring_q8_ok)
+        if (g.resid) return hipErrorInvalidValue;
+    } else if (g.resid) {
+        return g.bias ? launch_ring<R, ACT, true, fh::LN_NONE, true, 1, true>(g, s)
+                      : launch_ring<R, ACT, true, fh::LN_NONE, false, 1, true>(g, s);
+    }
+    return g.bias ? launch_ring<R, ACT, OUT_F32, fh::LN_NONE, true, 0, true>(g, s)
+                  : launch_ring<R, ACT, OUT_F32, fh::LN_NONE, false, 0, true>(g, s);
+}
+
+template <int ACT, bool OUT_F32>
+hipError_t launch_ring_q8(const GemmArgs &g, hipStream_t s) {
+    const bool fit256 = g.N % R5::BN == 0 && !g.resid;
+    const int c = ring_cfg();
+    if (c == 5 && fit256) return launch_ring_q8_r<R5, ACT, OUT_F32>(g, s);
+    if (c < 0 && fit256 && 4L * ((g.M + R5::BM - 1) / R5::BM) * (g.N / R5::BN) >= 3L * fh::cu_count())
+        return launch_ring_q8_r<R5, ACT, OUT_F32>(g, s);
+    return launch_ring_q8_r<R2, ACT, OUT_F32>(g, s);
+}
+
 // out row r ← B row ring_pack_row(r), 16 bytes per thread.
 __global__ void ring_pack_kernel(const f16 *__restrict__ B, f16 *__restrict__ out, int N, int K) {
     const long c = (long)blockIdx.x * blockDim.x + threadIdx.x, cpr = K / 8;
@@ -532,6 +582,23 @@ bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
     if (((double)g.M + BM_MAX) * g.lda * 2.0 >= 2147483648.0 || (double)g.N * g.ldb * 2.0 >= 2147483648.0) return false;
     if (((double)g.M + BM_MAX) * g.ldc * (out_f32 ? 4.0 : 2.0) >= 2147483648.0) return false;
     return true;
+}
+
+bool gemm_ring_q8_ok(const GemmArgs &g, int act, bool out_f32) {
+    if (g.M <= 0 || g.N % BN != 0 || g.K % 128 != 0 || g.K <= 0) return false;
+    if (act != ACT_NONE && act != ACT_GELU) return false;
+    if (!g.a_scale || !g.b_scale || g.resid_h || (g.resid && !out_f32)) return false;
+    if (g.lda % 16 || g.ldb % 16 || g.ldc % 8 || (g.resid && g.ldr % 4)) return false;
+    // 32-bit buffer offsets: every row the ring addresses (up to M + BM − 1).
+    if (((double)g.M + BM_MAX) * g.lda >= 2147483648.0 || (double)g.N * g.ldb >= 2147483648.0) return false;
+    if (((double)g.M + BM_MAX) * g.ldc * (out_f32 ? 4.0 : 2.0) >= 2147483648.0) return false;
+    return true;
+}
+
+hipError_t gemm_ring_q8(const GemmArgs &a, int act, bool out_f32, hipStream_t s) {
+    if (!gemm_ring_q8_ok(a, act, out_f32)) return hipErrorInvalidValue;
+    if (out_f32) return act == ACT_GELU ? launch_ring_q8<ACT_GELU, true>(a, s) : launch_ring_q8<ACT_NONE, true>(a, s);
+    return act == ACT_GELU ? launch_ring_q8<ACT_GELU, false>(a, s) : launch_ring_q8<ACT_NONE, false>(a, s);
 }
 
 hipError_t gemm_ring(const GemmArgs &a, int act, bool out_f32, hipStream_t s, int ln) {

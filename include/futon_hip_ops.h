@@ -44,6 +44,18 @@ int fh_op_gemm(int32_t dtype, const void *A, const void *B, const float *bias, c
 int fh_op_gemm_ring(const void *A, const void *B_packed, const float *bias, const void *resid, int32_t resid_f16,
                     void *C, int32_t M, int32_t N, int32_t K, int32_t act, int32_t out_f32, void *stream);
 
+/* The int8 contraction of fh_op_gemm (dtype I8: int8 codes A [M,K] and
+ * B [N,K] with per-row scales, f32 output C [M,N], bias and f32 residual
+ * optional) on the persistent LDS-ring kernel: B_packed is B's codes with
+ * their rows permuted by fh_op_ring_pack (which moves 16-byte units, so it
+ * takes the codes as a binary16 matrix of K/2 columns).  Requires
+ * N % 128 == 0 and K % 128 == 0; act is NONE or GELU.  Gives the same bits
+ * as fh_op_gemm with dtype I8.
+ * Replaces: q8Kernel.MatMulTQ8 (native/quant.go:92-137). */
+int fh_op_gemm_ring_q8(const void *A, const void *B_packed, const float *a_scale, const float *b_scale,
+                       const float *bias, const float *resid, float *C, int32_t M, int32_t N, int32_t K,
+                       int32_t act, void *stream);
+
 /* The folded-LayerNorm forms of the binary16 GEMM (K % 64 == 0), on the
  * tiled kernel (ring = 0, B as is) or the ring kernel (ring = 1, B packed);
  * stats holds [M] (mean, rstd) float pairs (fh_op_row_stats):

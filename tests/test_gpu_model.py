@@ -166,14 +166,15 @@ def test_gpu_matches_hf_bert_at_real_shapes(name):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192), ("bert-base", 24),
-                                        ("nomic-bert", 4)])
+                                        ("nomic-bert", 4), ("bge-small-q8", 256)])
 def test_ring_gemm_forward_equals_tiled(name, batch, monkeypatch):
     """The folded binary16 forward returns the same bits whether its
     projections run on the persistent ring GEMM (the default, at these
     5k-13k token batches; BERT-base's QKV and FFN1 and nomic-bert's SwiGLU
-    FFN1 on 256×256 tiles) or on the tiled GEMM (FUTON_GEMM_RING=0): same K
-    order, same LayerNorm statistics reduction, same epilogue arithmetic.
-    The CLS-pooled last layer (bge-small) runs tiled in both."""
+    FFN1 on 256×256 tiles; the Q8 path's int8 GEMMs on the ring's int8 form)
+    or on the tiled GEMM (FUTON_GEMM_RING=0): same K order, same LayerNorm
+    statistics reduction, same epilogue arithmetic.  The CLS-pooled last
+    layer (bge-small) runs tiled in both."""
     w = synth.workload(name)
     tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
     ids, offsets = synth.make_batch(w.ids_seed + 7, batch, w.len_lo, w.len_hi)

@@ -530,6 +530,38 @@ def test_q8_quantize_and_gemm_bit_exact(M, N, K):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 384, 384), (1030, 1536, 384), (2049, 384, 1536), (77, 128, 128),
+                                   (8269, 2048, 256)])
+def test_gemm_ring_q8_equals_tiled(M, N, K):
+    """The int8 form of the ring GEMM (int8 codes through the same LDS ring,
+    v_mfma_i32_16x16x64_i8, exact i32 sums scaled in the epilogue) returns
+    the tiled int8 kernel's bits: with bias and f32 residual, with GELU, and
+    plain; 8269×2048 takes the 256×256 layout on a 256-CU part."""
+    rng = np.random.default_rng(M + 7 * N + K)
+    qa = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    qb = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = (rng.random(M) * 0.02).astype(np.float32)
+    sb = (rng.random(N) * 0.001).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    r32 = rng.standard_normal((M, N)).astype(np.float32)
+    dqa, dqb, dsa, dsb, dbias, dr = dev(qa), dev(qb), dev(sa), dev(sb), dev(bias), dev(r32)
+    bp = torch.empty_like(dqb)
+    assert _lib().fh_op_ring_pack(ptr(dqb), ptr(bp), N, K // 2, None) == 0  # 16-byte units: codes as K/2 halves
+    sync()
+    assert np.array_equal(bp.cpu().numpy(), qb[ring_perm(N)])
+    for kw in (dict(bias=dbias, resid=dr), dict(bias=dbias, act=1), dict()):
+        want = gemm(1, dqa, dqb, a_scale=dsa, b_scale=dsb, **kw)
+        C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        rc = _lib().fh_op_gemm_ring_q8(ptr(dqa), ptr(bp), ptr(dsa), ptr(dsb), ptr(kw.get("bias")),
+                                       ptr(kw.get("resid")), ptr(C), M, N, K, kw.get("act", 0), None)
+        assert rc == 0
+        sync()
+        got = C.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (kw.keys(), np.abs(got - want).max())
+    exact = (qa.astype(np.int64) @ qb.astype(np.int64).T).astype(np.float64) * sa[:, None] * sb[None, :]
+    np.testing.assert_allclose(got.astype(np.float64), exact, rtol=1e-5, atol=1e-6)
+
+
 def attention_ref(qkv, offsets, heads, rope=None, q_limit=None):
     """float64 restatement of attendHead (native/model.go:646-701) per sequence."""
     T, H3 = qkv.shape
