@@ -124,6 +124,36 @@ __device__ __forceinline__ float rot(float x, float partner, float cs, float sn,
     return first ? a - b : a + b;
 }
 
+// rotateHalf applied in place to the binary16 Q and K of every token
+// (model.go:705-712): the same rot and rounding the attention kernels apply
+// while loading Q and staging K, so attention run afterwards without RoPE
+// gives the same bits, and K is rotated once per token instead of once per
+// query block that stages it.  Thread u of sequence blockIdx.y handles token
+// u / UPT of the sequence and one 8-wide chunk c of dims (c·8 .. +8, and the
+// partners half away) of one head of Q or of K; half % 8 == 0.
+__global__ __launch_bounds__(256) void rope_qk_kernel(f16 *__restrict__ qkv, const int32_t *__restrict__ offsets,
+                                                       int H, int d, const float *__restrict__ cos_t,
+                                                       const float *__restrict__ sin_t) {
+    const int seq = blockIdx.y, start = offsets[seq], L = offsets[seq + 1] - start;
+    const int half = d >> 1, cph = half / 8, heads = H / d, upt = 2 * heads * cph;
+    const long u = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= (long)L * upt) return;
+    const int p = (int)(u / upt), r = (int)(u - (long)p * upt);
+    const int region = r / (heads * cph), hc = r - region * heads * cph, head = hc / cph, c = hc - head * cph;
+    f16 *x = qkv + (size_t)(start + p) * 3 * H + region * H + head * d + c * 8;
+    const f16x8 a = *(const f16x8 *)x, b = *(const f16x8 *)(x + half);
+    const float *cp = cos_t + (size_t)p * half + c * 8, *sp = sin_t + (size_t)p * half + c * 8;
+    f16x8 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x1 = (float)a[e], x2 = (float)b[e], cs = cp[e], sn = sp[e];
+        lo[e] = (f16)rot(x1, x2, cs, sn, true);
+        hi[e] = (f16)rot(x2, x1, cs, sn, false);
+    }
+    *(f16x8 *)x = lo;
+    *(f16x8 *)(x + half) = hi;
+}
+
 // Q fragments of QT 16-query tiles (B operand of Sᵀ = K·Qᵀ): lane holds
 // dims [dk·32 + (lane/16)·8, +8) of query lane%16 of each tile, rotated
 // (rotateHalf, model.go:705-712) when the pack uses RoPE.
@@ -676,6 +706,18 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
 }  // namespace
 
 namespace fh {
+bool rope_qk_ok(int H, int d) { return d > 0 && H % d == 0 && (d / 2) % 8 == 0; }
+
+hipError_t rope_qk(f16 *qkv, const int32_t *offsets, int nseq, int max_len, int H, int d, const float *cos_t,
+                   const float *sin_t, hipStream_t s) {
+    if (!rope_qk_ok(H, d)) return hipErrorInvalidValue;
+    if (nseq <= 0 || max_len <= 0) return hipSuccess;
+    const long units = (long)max_len * 2 * (H / d) * (d / 16);
+    hipLaunchKernelGGL(rope_qk_kernel, dim3((unsigned)((units + 255) / 256), nseq), dim3(256), 0, s, qkv, offsets, H, d,
+                       cos_t, sin_t);
+    return hipGetLastError();
+}
+
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s) {
     if (nseq <= 0 || max_len <= 0) return hipSuccess;
     const bool rope = a.rope_cos != nullptr;

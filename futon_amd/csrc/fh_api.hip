@@ -924,6 +924,10 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             const double nq_l = last_cls ? (double)T : b.sum_l2;
             Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * 2,
                      s);
+            if (a.rope_cos && fh::rope_qk_ok(H, m->hd)) {  // as in run_forward
+                LCHK(fh::rope_qk(m->qkv, b.d_offsets, b.nseq, b.max_len, H, m->hd, m->rope_cos, m->rope_sin, s));
+                a.rope_cos = a.rope_sin = nullptr;
+            }
             LCHK(attend(a, b, false, s));
         }
 
@@ -1039,6 +1043,12 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
             const double nq_l = last_cls ? (double)T : b.sum_l2;  // Σ nq·L
             Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * (q8 ? 4 : 2),
                      s);
+            // RoPE: Q and K rotated once per token in place, then attention
+            // without it (the same bits as rotating inside attention).
+            if (a.rope_cos && fh::rope_qk_ok(H, m->hd)) {
+                LCHK(fh::rope_qk(m->qkv, b.d_offsets, b.nseq, b.max_len, H, m->hd, m->rope_cos, m->rope_sin, s));
+                a.rope_cos = a.rope_sin = nullptr;
+            }
             LCHK(attend(a, b, q8, s));
         }
 

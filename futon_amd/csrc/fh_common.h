@@ -182,6 +182,13 @@ hipError_t mlp(const MlpArgs &a, hipStream_t s);
 // two round differently, so a batch that mixes them is split (fh_encode).
 constexpr int ATTN_ONE_BLOCK_KEYS = 128;
 hipError_t attention(const AttnArgs &a, int nseq, int max_len, bool out_f32, hipStream_t s);
+// rotateHalf of every token's Q and K in place (binary16 qkv [T, 3H], head
+// width d, cos/sin tables [max_len, d/2]), with the rounding the attention
+// kernels apply when they rotate: attention then runs without RoPE and gives
+// the same bits.  Needs (d/2) % 8 == 0 (rope_qk_ok).
+bool rope_qk_ok(int H, int d);
+hipError_t rope_qk(f16 *qkv, const int32_t *offsets, int nseq, int max_len, int H, int d, const float *cos_t,
+                   const float *sin_t, hipStream_t s);
 // gamma == null (only for H/64 in {4, 6, 8, 12, 16}) writes the un-normalized
 // binary16 sum to x16 instead, for a consumer that folds this LayerNorm.
 // q non-null (with gamma and x32): also the int8 codes and scales of the
