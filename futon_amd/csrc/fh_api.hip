@@ -194,6 +194,10 @@ struct fh_model {
     fh_config cfg{};
     int device = 0, hd = 0, eff_max = 0;
     bool lnfold = false;  // LayerNorms folded into the GEMMs (binary16 path)
+    // Q and K rotated by rope_qk before attention (RoPE packs whose head width
+    // it covers); FUTON_ROPE_QK=0 leaves the rotation inside the attention
+    // kernels (diagnostics: the same bits either way).
+    bool rope_pre = false;
     hipStream_t stream = nullptr;
     float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -493,6 +497,8 @@ struct WsPlan {
     const std::pair<void **, size_t> *end() const { return e + n; }
     void push_back(std::pair<void **, size_t> p) { e[n++] = p; }
 };
+bool rope_pre(const fh_model *m) { return m->rope_pre; }
+
 WsPlan workspace_plan(fh_model *m, int T, int S) {
     const size_t H = (size_t)m->cfg.hidden_size, I = (size_t)m->cfg.intermediate_size;
     const bool q8 = m->cfg.q8 != 0;
@@ -924,7 +930,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             const double nq_l = last_cls ? (double)T : b.sum_l2;
             Scope sc(m, last_cls ? K_CLS_TAIL : K_ATTN, 4.0 * nq_l * H, (double)T * 3 * H * 2 + (last_cls ? S : T) * (double)H * 2,
                      s);
-            if (a.rope_cos && fh::rope_qk_ok(H, m->hd)) {  // as in run_forward
+            if (rope_pre(m)) {  // as in run_forward
                 LCHK(fh::rope_qk(m->qkv, b.d_offsets, b.nseq, b.max_len, H, m->hd, m->rope_cos, m->rope_sin, s));
                 a.rope_cos = a.rope_sin = nullptr;
             }
@@ -1045,7 +1051,7 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
                      s);
             // RoPE: Q and K rotated once per token in place, then attention
             // without it (the same bits as rotating inside attention).
-            if (a.rope_cos && fh::rope_qk_ok(H, m->hd)) {
+            if (rope_pre(m)) {
                 LCHK(fh::rope_qk(m->qkv, b.d_offsets, b.nseq, b.max_len, H, m->hd, m->rope_cos, m->rope_sin, s));
                 a.rope_cos = a.rope_sin = nullptr;
             }
@@ -1325,6 +1331,8 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
         if ((rc = upload(m, &m->rope_cos, cs.data(), cs.size() * 4)) ||
             (rc = upload(m, &m->rope_sin, sn.data(), sn.size() * 4)))
             return bail(rc);
+        const char *rq = getenv("FUTON_ROPE_QK");
+        m->rope_pre = !(rq && rq[0] == '0') && fh::rope_qk_ok(H, hd);
     }
     *out = m;
     return FH_OK;

@@ -190,6 +190,27 @@ def test_ring_gemm_forward_equals_tiled(name, batch, monkeypatch):
 
 
 @pytest.mark.gpu
+def test_rope_before_attention_equals_rope_inside(monkeypatch):
+    """RoPE packs rotate Q and K once per token before attention (rope_qk);
+    the forward returns the same bits as with the rotation inside the
+    attention kernels (FUTON_ROPE_QK=0), over both attention classes."""
+    w = synth.workload("nomic-bert")
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    parts = [synth.make_batch(w.ids_seed + 11 + i, 1, L, L)[0] for i, L in enumerate((100, 700, 20, 257))]
+    ids = np.concatenate(parts).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
+    native = _native()
+    pre = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    monkeypatch.setenv("FUTON_ROPE_QK", "0")
+    inside = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    a = pre.EncodePacked(ids, offsets, w.out_dim)
+    b = inside.EncodePacked(ids, offsets, w.out_dim)
+    assert np.array_equal(a, b), np.abs(a - b).max()
+    pre.close()
+    inside.close()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192)])
 def test_fused_mlp_forward_equals_two_gemms(name, batch, monkeypatch):
     """At hidden width 384 the feed-forward block runs as one fused kernel
