@@ -87,6 +87,20 @@ __device__ __forceinline__ float sum_xor32(float v) {
     return p[0] + p[1];
 }
 
+// Per query (lane%16), the sum of a key block's binary16 probabilities held
+// as the MFMA B operand (pf[c]: 32 keys per chunk): ones·Pᵀ on the matrix
+// cores, each row of the result tile the column sum.  Used where the block's
+// probabilities are summed for the softmax denominator (the kernels with
+// several key blocks); it normalizes by exactly the weights PV multiplies.
+template <int NC>
+__device__ __forceinline__ float prob_sum(const f16x8 (&pf)[NC]) {
+    const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[c], acc, 0, 0, 0);
+    return acc[0];
+}
+
 // Block ids reach the 8 XCDs round-robin; remap them so each XCD gets a
 // contiguous range of (query group, head, sequence) items, ordered so that
 // blocks which read the same qkv lines share one L2 (the lines are then
@@ -395,10 +409,14 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float p = kt < NV ? __builtin_amdgcn_exp2f(s[kt < NV ? kt : 0][i] * sl2 - m_new) : 0.f;
-                    psum += p;
+                    if (ONE) psum += p;
                     pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
                 }
-            psum = sum_xor32(sum_xor16(psum));
+            // Several key blocks: the block's probability sum per query on
+            // the matrix cores, from the binary16 probabilities PV uses
+            // (ones·Pᵀ, every row of the tile the sum), as attn_long_kernel.
+            if (ONE) psum = sum_xor32(sum_xor16(psum));
+            else psum = prob_sum<NC>(pf);
             l_run[st] = l_run[st] * corr + psum;
             m_run[st] = m_new;
 #pragma unroll
@@ -579,17 +597,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
         mx = max_xor32(max_xor16(mx));
         const float m_new = fmaxf(m_run[qt], mx * sl2);  // log2-scaled running max
         const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-        float psum = 0.f;
         f16x8 pf[NC];
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(s[kt][i] * sl2 - m_new);
-                psum += p;
-                pf[kt >> 1][(kt & 1) * 4 + i] = (f16)p;
-            }
-        psum = sum_xor32(sum_xor16(psum));
+            for (int i = 0; i < 4; ++i) pf[kt >> 1][(kt & 1) * 4 + i] = (f16)__builtin_amdgcn_exp2f(s[kt][i] * sl2 - m_new);
+        const float psum = prob_sum<NC>(pf);  // the block's sum of the binary16 probabilities
         l_run[qt] = l_run[qt] * corr + psum;
         m_run[qt] = m_new;
 #pragma unroll
