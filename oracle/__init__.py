@@ -2,8 +2,8 @@
 
 ctypes binding of ``oracle/liboracle.so`` (built from ``oracle/oracle.c`` by
 ``oracle/Makefile``).  Only ``tests/``, ``__graft_entry__.smoke()`` and
-``bench.py``'s ``cpu_baseline`` leg import this module, and only as the
-checker; nothing under ``futon_amd/`` may import it.
+``bench.py``'s ``cpu_baseline`` leg import this module, and only to compare
+against; nothing under ``futon_amd/`` may import it.
 
 Parity status of each function (how it is pinned; see ``tests/test_oracle.py``):
 

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the futon encoder forward pass — TEST INFRASTRUCTURE ONLY.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
- * it, as the checker; the product never does.
+ * it, to compare against; the product never does.
  *
  * Restates, in C, the reference's Go forward (native/model.go), its float32
  * transcendentals (native/mathf32.go), the amd64 AVX2 GEMM's per-element

@@ -2,7 +2,7 @@
  * CPU oracle for the futon encoder forward pass — TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference's Go CPU path, used by tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker.
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg, to compare against.
  * Nothing in the product (futon_amd/) links, loads or calls this code.
  *
  * Every function cites the reference file:line it follows.  Floating-point
