@@ -127,6 +127,25 @@ __device__ __forceinline__ void block_item(const AttnArgs &a, int &seq, int &hea
     seq += a.seq0;
 }
 
+// The long kernel's mapping at head widths of 64 and more (a head's q/k/v
+// segment is then a whole 128-byte line, so head pairs share nothing):
+// units u = (sequence, head) are dealt round-robin to the XCDs (unit u on XCD
+// u mod 8) and every query group of a unit runs on the unit's XCD, where its
+// K/V rows are fetched into one L2.  Each XCD thus gets interleaved heads of
+// every sequence and the same share of work whatever the sequence lengths
+// (contiguous ranges of sequences differ by up to 13% per XCD at 512..2048
+// tokens).  The 1-D grid holds gx·8·ceil(units/8) blocks; false: no unit.
+__device__ __forceinline__ bool block_unit(const AttnArgs &a, int gx, int units, int &seq, int &head, int &qg) {
+    const int pid = blockIdx.x, xcd = pid & 7, idx = pid >> 3;
+    const int u = xcd + 8 * (idx / gx);
+    qg = idx - (idx / gx) * gx;
+    if (u >= units) return false;
+    const int heads = a.H / a.d;
+    seq = u / heads + a.seq0;
+    head = u - (u / heads) * heads;
+    return true;
+}
+
 // rotateHalf's two products and their difference (first half) or sum
 // (second half), each rounded to float32 on its own as the reference's Go
 // code computes them, the same in every kernel: contraction into a fused
@@ -470,7 +489,7 @@ void attn_kernel(AttnArgs a) {
 // query tiles, so a block stages each key block once for 16·QT·WAVES
 // queries.
 template <int D, int WAVES, int QT, bool OUT_F32, bool ROPE>
-__global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a, int gx, int units) {
     constexpr int BK = 64, NKT = BK / 16, NC = BK / 32;
     constexpr int NT = WAVES * 64, QROWS = 16 * QT * WAVES;
     constexpr int KS = D + 8, VS = BK + 8;  // LDS row pitches (halves)
@@ -483,7 +502,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) f16 Vt[2][D * VS];
 
     int seq, head, qg;
-    block_item(a, seq, head, qg);
+    if (D >= 64 && units > 0) {
+        if (!block_unit(a, gx, units, seq, head, qg)) return;
+    } else {
+        block_item(a, seq, head, qg);
+    }
     const int start = a.offsets[seq];
     const int L = a.offsets[seq + 1] - start;
     const int nq = min(L, a.q_limit);
@@ -668,14 +691,20 @@ template <int D, int WAVES, int QT>
 hipError_t launch_long(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool rope, hipStream_t s) {
     constexpr int QROWS = 16 * QT * WAVES;
     const int qmax = min(max_len, a.q_limit);
-    dim3 grid((qmax + QROWS - 1) / QROWS, a.H / a.d, nseq);
+    const int gx = (qmax + QROWS - 1) / QROWS;
+    // D ≥ 64: (sequence, head) units dealt to the XCDs (block_unit) while the
+    // 1-D grid's work-items fit 32 bits; else (units = 0) block_item's
+    // (query group, head, sequence) grid.
+    const long nblk = (long)gx * (((long)a.H / a.d * nseq + 7) / 8 * 8);
+    const int units = D >= 64 && nblk * (WAVES * 64) < (1l << 32) ? a.H / a.d * nseq : 0;
+    dim3 grid = units ? dim3((unsigned)nblk) : dim3(gx, a.H / a.d, nseq);
     dim3 block(WAVES * 64);
     if (out_f32) {
-        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, true>), grid, block, 0, s, a, gx, units);
+        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, true, false>), grid, block, 0, s, a, gx, units);
     } else {
-        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, false>), grid, block, 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, true>), grid, block, 0, s, a, gx, units);
+        else hipLaunchKernelGGL((attn_long_kernel<D, WAVES, QT, false, false>), grid, block, 0, s, a, gx, units);
     }
     return hipGetLastError();
 }
