@@ -644,26 +644,35 @@ __global__ __launch_bounds__(WAVES * 64) void attn_long_kernel(AttnArgs a, int g
         }
     };
 
+    // Every key block but the last is full and has a successor, so the loop
+    // body is one straight path (a branch between the full and the masked
+    // copy inside it made the compiler shuffle the loop-carried registers,
+    // ~56 moves per key block); the last block follows the loop.
     const int nkb = (L + BK - 1) / BK;
     load_kv(0);
     store_kv(0, 0);
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
+    for (int kb = 0; kb + 1 < nkb; ++kb) {
         const int kb0 = kb * BK, buf = kb & 1;
-        const bool more = kb + 1 < nkb;
-        if (more) load_kv(kb0 + BK);  // in flight while this block is multiplied
+        load_kv(kb0 + BK);  // in flight while this block is multiplied
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+            if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, BK, std::false_type{});  // wave-uniform
+        // The other buffer was last read before the previous barrier.
+        store_kv(buf ^ 1, kb0 + BK);
+        __syncthreads();
+    }
+    {
+        const int kb0 = (nkb - 1) * BK, buf = (nkb - 1) & 1;
         if (L - kb0 >= BK) {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt)
-                if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, BK, std::false_type{});  // wave-uniform
+                if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, BK, std::false_type{});
         } else {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt)
                 if (q0 + (wave * QT + qt) * 16 < nq) qtile(qt, buf, L - kb0, std::true_type{});
         }
-        // The other buffer was last read before the previous barrier.
-        if (more) store_kv(buf ^ 1, kb0 + BK);
-        __syncthreads();
     }
 
     // Lane owns O[query lane%16][dims t·16 + (lane/16)·4 .. +4] of each tile.
