@@ -30,11 +30,10 @@ namespace {
 #ifndef ATTN_ONE_WAVES
 #define ATTN_ONE_WAVES 6
 #endif
-#ifndef ATTN_LONG_WAVES
-#define ATTN_LONG_WAVES 4
-#endif
-#ifndef ATTN_LONG_QT
-#define ATTN_LONG_QT 2
+// Long-kernel block shapes (waves × query tiles per wave): 8 × 2 while the
+// longest sequence has at most ATTN_LONG_SPLIT tokens, 4 × 3 beyond.
+#ifndef ATTN_LONG_SPLIT
+#define ATTN_LONG_SPLIT 1024
 #endif
 
 // Sequences past one key block take the pipelined kernel (attn_long_kernel)
@@ -750,7 +749,16 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
     if (max_len <= 64) return launch_d<D, 2, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
     // Up to 128 tokens: one block covers every query and stages K/V once.
     if (max_len <= fh::ATTN_ONE_BLOCK_KEYS) return launch_d<D, 4, 2, 128, true>(a, nseq, max_len, out_f32, rope, s);
-    if (a.d == D && long_pipeline()) return launch_long<D, ATTN_LONG_WAVES, ATTN_LONG_QT>(a, nseq, max_len, out_f32, rope, s);
+    if (a.d == D && long_pipeline()) {
+        // Same per-query arithmetic (same bits) in either shape.  Up to 1024
+        // tokens, 256-query blocks of 8 waves (BERT-base, 512 tokens: 2.59 →
+        // 2.40 ms per step against 4 × 2); beyond, three query tiles per wave
+        // share each K/V fragment read and key-block barrier (nomic-bert,
+        // 540..2021 tokens: 3.08 → 2.83 ms against 4 × 2, while 8 × 2 gains
+        // nothing there).
+        if (max_len > ATTN_LONG_SPLIT) return launch_long<D, 4, 3>(a, nseq, max_len, out_f32, rope, s);
+        return launch_long<D, 8, 2>(a, nseq, max_len, out_f32, rope, s);
+    }
     return launch_d<D, 4, 1, 64, false>(a, nseq, max_len, out_f32, rope, s);
 }
 

@@ -645,6 +645,8 @@ def test_attention_matches_float64(H, heads, lens, rope):
     (384, 12, [130, 257], True),
     (768, 12, [512, 77, 512], False),
     (768, 12, [2048, 300, 700, 129], True),
+    (768, 12, [1100, 513, 64], False),
+    (384, 12, [1500, 200], False),
     (1536, 12, [200, 129, 64], True),
 ])
 @pytest.mark.parametrize("out_f32", [0, 1])
