@@ -30,8 +30,9 @@ namespace {
 #ifndef ATTN_ONE_WAVES
 #define ATTN_ONE_WAVES 6
 #endif
-// Long-kernel block shapes (waves × query tiles per wave): 8 × 2 while the
-// longest sequence has at most ATTN_LONG_SPLIT tokens, 4 × 3 beyond.
+// Long-kernel block shapes (waves × query tiles per wave) at head width 64:
+// 8 × 2 while the longest sequence has at most ATTN_LONG_SPLIT tokens, 4 × 3
+// beyond; 4 × 2 at head width 32.
 #ifndef ATTN_LONG_SPLIT
 #define ATTN_LONG_SPLIT 1024
 #endif
@@ -756,6 +757,9 @@ hipError_t launch_w(const AttnArgs &a, int nseq, int max_len, bool out_f32, bool
         // share each K/V fragment read and key-block barrier (nomic-bert,
         // 540..2021 tokens: 3.08 → 2.83 ms against 4 × 2, while 8 × 2 gains
         // nothing there).
+        // At head width 32, 8 × 2 measured no faster than 4 × 2 (bge-small,
+        // a mixed batch of 2..512 tokens).
+        if (D < 64) return launch_long<D, 4, 2>(a, nseq, max_len, out_f32, rope, s);
         if (max_len > ATTN_LONG_SPLIT) return launch_long<D, 4, 3>(a, nseq, max_len, out_f32, rope, s);
         return launch_long<D, 8, 2>(a, nseq, max_len, out_f32, rope, s);
     }
