@@ -198,6 +198,11 @@ struct fh_model {
     // it covers); FUTON_ROPE_QK=0 leaves the rotation inside the attention
     // kernels (diagnostics: the same bits either way).
     bool rope_pre = false;
+    // Mean pooling takes the last hidden state un-normalized and applies its
+    // LayerNorm inside the segment sums (fh::ln_pool), for the widths that
+    // kernel covers; FUTON_LN_POOL=0 keeps the LayerNorm and the pooling
+    // apart (diagnostics; the segment sums are then added in another order).
+    bool ln_pool = false;
     hipStream_t stream = nullptr;
     float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -498,6 +503,8 @@ struct WsPlan {
     void push_back(std::pair<void **, size_t> p) { e[n++] = p; }
 };
 bool rope_pre(const fh_model *m) { return m->rope_pre; }
+// Mean pooling through fh::ln_pool for this model (its last LayerNorm fused).
+bool ln_pool_on(const fh_model *m) { return m->ln_pool && m->cfg.pooling != FH_POOL_CLS; }
 
 WsPlan workspace_plan(fh_model *m, int T, int S) {
     const size_t H = (size_t)m->cfg.hidden_size, I = (size_t)m->cfg.intermediate_size;
@@ -979,8 +986,15 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             return rc;
         if ((rc = gemm_resln(m, kFc2, L.fc2, m->hbuf, M, L.fc2_b, yBo, sB, L.n1w, L.n1b, yA, s))) return rc;
     }
-    // The last norm2, to f32 rows for pooling.
+    // The last norm2, to f32 rows for pooling (or inside the mean pooling).
     const DevLayer &Lz = m->layers.back();
+    if (ln_pool_on(m)) {
+        const int od = b.out_dim == 0 ? H : b.out_dim;
+        Scope sc(m, K_POOL, 0.0, (double)T * H * 2 + (double)S * od * 4, s);
+        LCHK(fh::ln_pool(nullptr, m->x16, b.d_offsets, S, b.max_len, H, Lz.n2w, Lz.n2b, (float)c.layer_norm_eps,
+                         c.matryoshka_layernorm, od, c.normalize, m->pool_part, b.d_out, s));
+        return FH_OK;
+    }
     if ((rc = layer_norm(m, K_LN, nullptr, cls ? m->xc16 : m->x16, cls ? S : T, Lz.n2w, Lz.n2b, cls ? m->xc32 : m->x32,
                          nullptr, s)))
         return rc;
@@ -1106,7 +1120,16 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
                       false, s);
         }
         if (rc) return rc;
-        // norm2; Q8: with the next layer's QKV activation codes
+        // norm2; Q8: with the next layer's QKV activation codes.  The last
+        // one is left to the mean pooling when that fuses it.
+        if (last && ln_pool_on(m)) {
+            const int od = b.out_dim == 0 ? H : b.out_dim;
+            Scope sc(m, K_POOL, 0.0, (double)T * H * (f32res ? 4 : 2) + (double)S * od * 4, s);
+            LCHK(fh::ln_pool(f32res ? m->y32 : nullptr, f32res ? nullptr : y16, b.d_offsets, S, b.max_len, H,
+                             L.n2w, L.n2b, (float)c.layer_norm_eps, c.matryoshka_layernorm, od, c.normalize,
+                             m->pool_part, b.d_out, s));
+            return FH_OK;
+        }
         if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n2w, L.n2b,
                              (f32res || last) ? xo32 : nullptr, xo16, s, q8 && !last)))
             return rc;
@@ -1333,6 +1356,10 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
             return bail(rc);
         const char *rq = getenv("FUTON_ROPE_QK");
         m->rope_pre = !(rq && rq[0] == '0') && fh::rope_qk_ok(H, hd);
+    }
+    {
+        const char *lp = getenv("FUTON_LN_POOL");
+        m->ln_pool = !(lp && lp[0] == '0') && fh::ln_pool_ok(H);
     }
     *out = m;
     return FH_OK;

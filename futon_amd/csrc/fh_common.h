@@ -221,4 +221,12 @@ __host__ __device__ inline int64_t pool_part_row(int64_t start, int64_t seq) { r
 inline int64_t pool_part_rows(int64_t T, int64_t nseq) { return T / POOL_SEG + nseq + 1; }
 hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int max_len, int H, int cls_compact,
                 int mean, int matryoshka_ln, int out_dim, int normalize, float *part, float *out, hipStream_t s);
+// Mean pooling straight from the un-normalized last hidden state (binary16
+// y16 or float32 y32, [T, H]): its LayerNorm (γ, β, eps) fused with the
+// segment sums, then pool's per-sequence stage.  H / 64 ∈ {4, 6, 8, 12, 16}
+// (ln_pool_ok).
+bool ln_pool_ok(int H);
+hipError_t ln_pool(const float *y32, const f16 *y16, const int32_t *offsets, int nseq, int max_len, int H,
+                   const float *gamma, const float *beta, float eps, int matryoshka_ln, int out_dim, int normalize,
+                   float *part, float *out, hipStream_t s);
 }  // namespace fh

@@ -240,13 +240,11 @@ __global__ __launch_bounds__(256) void quantize_rows_v_kernel(const float *x, in
     quant_row_v<VPL>(v, lane, q + (size_t)row * (64 * VPL), scale + row);
 }
 
-// Normalizes v in place with statistics of the row and writes it out; gw/gb
-// hold this lane's γ/β elements.
+// Normalizes v (a row in ld_row's layout) in place with statistics of the
+// row; gw/gb hold this lane's γ/β elements.
 template <int VPL>
-__device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL], const float (&gb)[VPL], float eps,
-                                         float *o32, f16 *o16) {
+__device__ __forceinline__ void ln_norm_v(float (&v)[VPL], const float (&gw)[VPL], const float (&gb)[VPL], float eps) {
     constexpr int H = 64 * VPL;
-    const int lane = threadIdx.x & 63;
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) s += v[j];
@@ -261,7 +259,19 @@ __device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL]
     const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) v[j] = (v[j] - mean) * inv * gw[j] + gb[j];
-    st_row<VPL>(o32, o16, lane, v);
+}
+// ln_norm_v, then the row written out.
+template <int VPL>
+__device__ __forceinline__ void ln_row_v(float (&v)[VPL], const float (&gw)[VPL], const float (&gb)[VPL], float eps,
+                                         float *o32, f16 *o16) {
+    ln_norm_v<VPL>(v, gw, gb, eps);
+    st_row<VPL>(o32, o16, threadIdx.x & 63, v);
+}
+// Column of element j of a lane's row in ld_row's layout.
+template <int VPL>
+__device__ __forceinline__ int row_col(int j, int lane) {
+    constexpr int N4 = VPL / 4;
+    return j < 4 * N4 ? 4 * (64 * (j >> 2) + lane) + (j & 3) : 256 * N4 + 2 * lane + (j - 4 * N4);
 }
 
 // (mean, rstd) per row of binary16 y [M, 128·C]: 16 lanes per row, C
@@ -392,6 +402,58 @@ __global__ __launch_bounds__(256) void pool_partial_kernel(const float *__restri
             for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], v[i]);
         }
         *(f32x4 *)(dst + c) = acc;
+    }
+}
+
+// The last LayerNorm fused with mean pooling's first stage, for the pooled
+// rows only: block (segment j, sequence q) with 8 waves; wave w normalizes
+// rows t0 + 8w .. t0 + 8w + 7 of the segment (layer_norm_v's arithmetic,
+// ln_norm_v) and adds them up per column in token order, then the waves'
+// sums are added in wave order into the segment's partial row (pool_part_row,
+// as pool_partial_kernel).  The normalized rows are never written: the
+// float32 hidden state of every token (4H bytes a token) is neither stored
+// nor read back.  The order of the sums depends only on the sequence, not on
+// the rest of the batch.
+template <int VPL, class T>
+__global__ __launch_bounds__(512) void ln_pool_partial_kernel(const T *__restrict__ y,
+                                                              const int32_t *__restrict__ offsets,
+                                                              const float *__restrict__ gamma,
+                                                              const float *__restrict__ beta, float eps,
+                                                              float *__restrict__ part) {
+    constexpr int H = 64 * VPL, NWV = 8, RW = fh::POOL_SEG / NWV;
+    __shared__ float wsum[NWV][H];
+    const int seq = blockIdx.y, j = blockIdx.x;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    const int t0 = j * fh::POOL_SEG;
+    if (t0 >= L) return;  // the whole block
+    const int t1 = min(L, t0 + fh::POOL_SEG);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = t0 + wave * RW, n = min(t1 - r0, RW);  // this wave's rows (none when n ≤ 0)
+    if (n > 0) {
+        float gw[VPL], gb[VPL], v[RW][VPL], acc[VPL];
+        ld_row<VPL>(gamma, lane, gw);
+        ld_row<VPL>(beta, lane, gb);
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            if (r < n) ld_row<VPL>(y + (size_t)(start + r0 + r) * H, lane, v[r]);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            if (r < n) {
+                ln_norm_v<VPL>(v[r], gw, gb, eps);
+#pragma unroll
+                for (int i = 0; i < VPL; ++i) acc[i] = r == 0 ? v[0][i] : __fadd_rn(acc[i], v[r][i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) wsum[wave][row_col<VPL>(i, lane)] = acc[i];
+    }
+    __syncthreads();
+    const int nw = (t1 - t0 + RW - 1) / RW;  // waves that had rows
+    float *dst = part + (size_t)(fh::pool_part_row(start, seq) + j) * H;
+    for (int c = threadIdx.x; c < H; c += NWV * 64) {
+        float sum = wsum[0][c];
+        for (int w = 1; w < nw; ++w) sum = __fadd_rn(sum, wsum[w][c]);
+        dst[c] = sum;
     }
 }
 
@@ -536,6 +598,29 @@ hipError_t quantize_rows(const float *x, int M, int K, int ldx, int8_t *q, float
     }
 #undef FH_Q_V
     hipLaunchKernelGGL(quantize_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, M, K, ldx, q, scale);
+    return hipGetLastError();
+}
+bool ln_pool_ok(int H) { return H % 64 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16); }
+hipError_t ln_pool(const float *y32, const f16 *y16, const int32_t *offsets, int nseq, int max_len, int H,
+                   const float *gamma, const float *beta, float eps, int matryoshka_ln, int out_dim, int normalize,
+                   float *part, float *out, hipStream_t s) {
+    if (nseq <= 0) return hipSuccess;
+    if (!ln_pool_ok(H) || !part || max_len <= 0 || !gamma || !beta || !(y32 || y16)) return hipErrorInvalidValue;
+    const dim3 grid((max_len + POOL_SEG - 1) / POOL_SEG, nseq);
+#define FH_LNP(V)                                                                                                  \
+    case V:                                                                                                        \
+        if (y16) hipLaunchKernelGGL((ln_pool_partial_kernel<V, f16>), grid, dim3(512), 0, s, y16, offsets, gamma,   \
+                                    beta, eps, part);                                                              \
+        else hipLaunchKernelGGL((ln_pool_partial_kernel<V, float>), grid, dim3(512), 0, s, y32, offsets, gamma,     \
+                                beta, eps, part);                                                                  \
+        break;
+    switch (H / 64) {
+        FH_LNP(4) FH_LNP(6) FH_LNP(8) FH_LNP(12) FH_LNP(16)
+    default: return hipErrorInvalidValue;
+    }
+#undef FH_LNP
+    hipLaunchKernelGGL(pool_kernel, dim3(nseq), dim3(256), 0, s, (const float *)nullptr, part, offsets, H, 0, 1,
+                       matryoshka_ln, out_dim, normalize, out);
     return hipGetLastError();
 }
 hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int max_len, int H, int cls_compact, int mean,

@@ -211,6 +211,34 @@ def test_rope_before_attention_equals_rope_inside(monkeypatch):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name,lens", [("minilm-l6", (100, 7, 64, 65, 128, 1)), ("nomic-bert", (700, 20, 257, 129))])
+def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
+    """Mean pooling applies the last LayerNorm inside its segment sums
+    (fh::ln_pool); with FUTON_LN_POOL=0 the LayerNorm writes the float32
+    rows and the pooling reads them back.  Same normalized values, summed in
+    another order (eight-row groups inside each 64-token segment), so the
+    vectors agree to float32 rounding, and batch ≡ single still holds."""
+    w = synth.workload(name)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    parts = [synth.make_batch(w.ids_seed + 21 + i, 1, L, L)[0] for i, L in enumerate(lens)]
+    ids = np.concatenate(parts).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
+    native = _native()
+    fused = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    monkeypatch.setenv("FUTON_LN_POOL", "0")
+    apart = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    a = fused.EncodePacked(ids, offsets, w.out_dim)
+    b = apart.EncodePacked(ids, offsets, w.out_dim)
+    assert np.abs(a - b).max() < 2e-6, np.abs(a - b).max()
+    cos = np.sum(a * b, axis=1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+    assert cos.min() > 0.9999999, cos.min()
+    single = fused.EncodePacked(parts[1], np.array([0, len(parts[1])], dtype=np.int32), w.out_dim)
+    assert np.array_equal(single[0].view(np.uint32), a[1].view(np.uint32))
+    fused.close()
+    apart.close()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192)])
 def test_fused_mlp_forward_equals_two_gemms(name, batch, monkeypatch):
     """At hidden width 384 the feed-forward block runs as one fused kernel
