@@ -198,10 +198,11 @@ struct fh_model {
     // it covers); FUTON_ROPE_QK=0 leaves the rotation inside the attention
     // kernels (diagnostics: the same bits either way).
     bool rope_pre = false;
-    // Mean pooling takes the last hidden state un-normalized and applies its
-    // LayerNorm inside the segment sums (fh::ln_pool), for the widths that
-    // kernel covers; FUTON_LN_POOL=0 keeps the LayerNorm and the pooling
-    // apart (diagnostics; the segment sums are then added in another order).
+    // Pooling takes the last hidden state un-normalized and applies its
+    // LayerNorm itself (mean: inside the segment sums, fh::ln_pool; CLS: on
+    // the compact rows, fh::ln_cls_pool), for the widths those kernels cover;
+    // FUTON_LN_POOL=0 keeps the LayerNorm and the pooling apart (diagnostics;
+    // for mean pooling the segment sums are then added in another order).
     bool ln_pool = false;
     hipStream_t stream = nullptr;
     float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
@@ -503,8 +504,7 @@ struct WsPlan {
     void push_back(std::pair<void **, size_t> p) { e[n++] = p; }
 };
 bool rope_pre(const fh_model *m) { return m->rope_pre; }
-// Mean pooling through fh::ln_pool for this model (its last LayerNorm fused).
-bool ln_pool_on(const fh_model *m) { return m->ln_pool && m->cfg.pooling != FH_POOL_CLS; }
+
 
 WsPlan workspace_plan(fh_model *m, int T, int S) {
     const size_t H = (size_t)m->cfg.hidden_size, I = (size_t)m->cfg.intermediate_size;
@@ -884,6 +884,25 @@ int layer_norm(fh_model *m, int cls, const float *y32, const f16 *y16, int M, co
     return FH_OK;
 }
 
+// The pooling stage applies the last LayerNorm (fh::ln_pool / ln_cls_pool)
+// from y32 or y16: the un-normalized last hidden state, all T rows (mean) or
+// the S compact CLS rows.
+int pool_with_ln(fh_model *m, const BatchInfo &b, const float *y32, const f16 *y16, const float *gw, const float *gb,
+                 hipStream_t s) {
+    const fh_config &c = m->cfg;
+    const int H = c.hidden_size, S = b.nseq, od = b.out_dim == 0 ? H : b.out_dim;
+    const bool cls = c.pooling == FH_POOL_CLS;
+    const double rows = cls ? (double)S : (double)b.T;
+    Scope sc(m, K_POOL, 0.0, rows * H * (y32 ? 4 : 2) + (double)S * od * 4, s);
+    if (cls)
+        LCHK(fh::ln_cls_pool(y32, y16, S, H, gw, gb, (float)c.layer_norm_eps, c.matryoshka_layernorm, od, c.normalize,
+                             b.d_out, s));
+    else
+        LCHK(fh::ln_pool(y32, y16, b.d_offsets, S, b.max_len, H, gw, gb, (float)c.layer_norm_eps,
+                         c.matryoshka_layernorm, od, c.normalize, m->pool_part, b.d_out, s));
+    return FH_OK;
+}
+
 // Forward with every LayerNorm but the last folded into the GEMMs (binary16
 // path).  The residual stream is carried un-normalized: yA (x16) is the input
 // of the LayerNorm that feeds the attention block (the embedding sum, then
@@ -988,13 +1007,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
     }
     // The last norm2, to f32 rows for pooling (or inside the mean pooling).
     const DevLayer &Lz = m->layers.back();
-    if (ln_pool_on(m)) {
-        const int od = b.out_dim == 0 ? H : b.out_dim;
-        Scope sc(m, K_POOL, 0.0, (double)T * H * 2 + (double)S * od * 4, s);
-        LCHK(fh::ln_pool(nullptr, m->x16, b.d_offsets, S, b.max_len, H, Lz.n2w, Lz.n2b, (float)c.layer_norm_eps,
-                         c.matryoshka_layernorm, od, c.normalize, m->pool_part, b.d_out, s));
-        return FH_OK;
-    }
+    if (m->ln_pool) return pool_with_ln(m, b, nullptr, cls ? m->xc16 : m->x16, Lz.n2w, Lz.n2b, s);
     if ((rc = layer_norm(m, K_LN, nullptr, cls ? m->xc16 : m->x16, cls ? S : T, Lz.n2w, Lz.n2b, cls ? m->xc32 : m->x32,
                          nullptr, s)))
         return rc;
@@ -1122,14 +1135,8 @@ int run_forward(fh_model *m, const BatchInfo &b, hipStream_t s) {
         if (rc) return rc;
         // norm2; Q8: with the next layer's QKV activation codes.  The last
         // one is left to the mean pooling when that fuses it.
-        if (last && ln_pool_on(m)) {
-            const int od = b.out_dim == 0 ? H : b.out_dim;
-            Scope sc(m, K_POOL, 0.0, (double)T * H * (f32res ? 4 : 2) + (double)S * od * 4, s);
-            LCHK(fh::ln_pool(f32res ? m->y32 : nullptr, f32res ? nullptr : y16, b.d_offsets, S, b.max_len, H,
-                             L.n2w, L.n2b, (float)c.layer_norm_eps, c.matryoshka_layernorm, od, c.normalize,
-                             m->pool_part, b.d_out, s));
-            return FH_OK;
-        }
+        if (last && m->ln_pool)
+            return pool_with_ln(m, b, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, L.n2w, L.n2b, s);
         if ((rc = layer_norm(m, kLn, f32res ? m->y32 : nullptr, f32res ? nullptr : y16, M, L.n2w, L.n2b,
                              (f32res || last) ? xo32 : nullptr, xo16, s, q8 && !last)))
             return rc;

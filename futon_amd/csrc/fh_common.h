@@ -229,4 +229,8 @@ bool ln_pool_ok(int H);
 hipError_t ln_pool(const float *y32, const f16 *y16, const int32_t *offsets, int nseq, int max_len, int H,
                    const float *gamma, const float *beta, float eps, int matryoshka_ln, int out_dim, int normalize,
                    float *part, float *out, hipStream_t s);
+// CLS pooling of the compact last-layer rows [nseq, H] with their LayerNorm
+// (the same values as layer_norm then pool with cls_compact); H as ln_pool.
+hipError_t ln_cls_pool(const float *y32, const f16 *y16, int nseq, int H, const float *gamma, const float *beta,
+                       float eps, int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s);
 }  // namespace fh

@@ -461,27 +461,10 @@ __global__ __launch_bounds__(512) void ln_pool_partial_kernel(const T *__restric
 // CLS reads row seq of the compact last-layer buffer; mean adds the
 // sequence's segment sums (pool_partial_kernel) in segment order in float32
 // and scales by float32(1/L).
-__global__ __launch_bounds__(256) void pool_kernel(const float *x32, const float *part, const int32_t *offsets,
-                                                   int H, int cls_compact, int mean, int mat_ln, int out_dim,
-                                                   int normalize, float *out) {
-    __shared__ float pooled[1024];
-    __shared__ double red[4];
-    const int seq = blockIdx.x;
-    const int start = offsets[seq], L = offsets[seq + 1] - start;
-    for (int e = threadIdx.x; e < H; e += blockDim.x) {
-        float p;
-        if (mean) {
-            const int nseg = (L + fh::POOL_SEG - 1) / fh::POOL_SEG;
-            const float *col = part + (size_t)fh::pool_part_row(start, seq) * H + e;
-            p = col[0];
-            for (int j = 1; j < nseg; ++j) p = __fadd_rn(p, col[(size_t)j * H]);
-            p = __fmul_rn(p, __fdiv_rn(1.0f, (float)L));
-        } else {
-            p = x32[(size_t)(cls_compact ? seq : start) * H + e];
-        }
-        pooled[e] = p;
-    }
-    __syncthreads();
+// Matryoshka truncation (with its LayerNorm when asked) and L2 of the pooled
+// row in pooled[0..H) (every thread of the block calls it), into out[0..n).
+__device__ void finish_pooled(float *pooled, double *red, int H, int mat_ln, int out_dim, int normalize,
+                              float *out) {
     int n = H;
     if (out_dim != H) {
         if (mat_ln) {
@@ -510,8 +493,58 @@ __global__ __launch_bounds__(256) void pool_kernel(const float *x32, const float
         ss = block_sum_f64(ss, red);
         if (ss > 0) inv = (float)(1.0 / sqrt(ss));
     }
-    for (int e = threadIdx.x; e < n; e += blockDim.x)
-        out[(size_t)seq * n + e] = normalize ? __fmul_rn(pooled[e], inv) : pooled[e];
+    for (int e = threadIdx.x; e < n; e += blockDim.x) out[e] = normalize ? __fmul_rn(pooled[e], inv) : pooled[e];
+}
+
+__global__ __launch_bounds__(256) void pool_kernel(const float *x32, const float *part, const int32_t *offsets,
+                                                   int H, int cls_compact, int mean, int mat_ln, int out_dim,
+                                                   int normalize, float *out) {
+    __shared__ float pooled[1024];
+    __shared__ double red[4];
+    const int seq = blockIdx.x;
+    const int start = offsets[seq], L = offsets[seq + 1] - start;
+    for (int e = threadIdx.x; e < H; e += blockDim.x) {
+        float p;
+        if (mean) {
+            const int nseg = (L + fh::POOL_SEG - 1) / fh::POOL_SEG;
+            const float *col = part + (size_t)fh::pool_part_row(start, seq) * H + e;
+            p = col[0];
+            for (int j = 1; j < nseg; ++j) p = __fadd_rn(p, col[(size_t)j * H]);
+            p = __fmul_rn(p, __fdiv_rn(1.0f, (float)L));
+        } else {
+            p = x32[(size_t)(cls_compact ? seq : start) * H + e];
+        }
+        pooled[e] = p;
+    }
+    __syncthreads();
+    finish_pooled(pooled, red, H, mat_ln, out_dim, normalize, out + (size_t)seq * (out_dim != H ? out_dim : H));
+}
+
+// CLS pooling of the compact last-layer rows yc [nseq, H] (binary16, or
+// float32 on the Q8 path) with their LayerNorm: one wave normalizes the row
+// with layer_norm_v's arithmetic (ln_norm_v) into LDS, then finish_pooled.
+// The same values as the LayerNorm kernel followed by pool_kernel, without
+// the float32 row written and read back or the launch between them.
+template <int VPL, class T>
+__global__ __launch_bounds__(256) void ln_cls_pool_kernel(const T *__restrict__ yc, const float *__restrict__ gamma,
+                                                          const float *__restrict__ beta, float eps, int mat_ln,
+                                                          int out_dim, int normalize, float *out) {
+    constexpr int H = 64 * VPL;
+    __shared__ float pooled[H];
+    __shared__ double red[4];
+    const int seq = blockIdx.x;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float v[VPL], gw[VPL], gb[VPL];
+        ld_row<VPL>(yc + (size_t)seq * H, lane, v);
+        ld_row<VPL>(gamma, lane, gw);
+        ld_row<VPL>(beta, lane, gb);
+        ln_norm_v<VPL>(v, gw, gb, eps);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) pooled[row_col<VPL>(i, lane)] = v[i];
+    }
+    __syncthreads();
+    finish_pooled(pooled, red, H, mat_ln, out_dim, normalize, out + (size_t)seq * (out_dim != H ? out_dim : H));
 }
 
 }  // namespace
@@ -621,6 +654,24 @@ hipError_t ln_pool(const float *y32, const f16 *y16, const int32_t *offsets, int
 #undef FH_LNP
     hipLaunchKernelGGL(pool_kernel, dim3(nseq), dim3(256), 0, s, (const float *)nullptr, part, offsets, H, 0, 1,
                        matryoshka_ln, out_dim, normalize, out);
+    return hipGetLastError();
+}
+hipError_t ln_cls_pool(const float *y32, const f16 *y16, int nseq, int H, const float *gamma, const float *beta,
+                       float eps, int matryoshka_ln, int out_dim, int normalize, float *out, hipStream_t s) {
+    if (nseq <= 0) return hipSuccess;
+    if (!ln_pool_ok(H) || !gamma || !beta || !(y32 || y16)) return hipErrorInvalidValue;
+#define FH_LNC(V)                                                                                                \
+    case V:                                                                                                      \
+        if (y16) hipLaunchKernelGGL((ln_cls_pool_kernel<V, f16>), dim3(nseq), dim3(256), 0, s, y16, gamma, beta, \
+                                    eps, matryoshka_ln, out_dim, normalize, out);                                \
+        else hipLaunchKernelGGL((ln_cls_pool_kernel<V, float>), dim3(nseq), dim3(256), 0, s, y32, gamma, beta,   \
+                                eps, matryoshka_ln, out_dim, normalize, out);                                    \
+        break;
+    switch (H / 64) {
+        FH_LNC(4) FH_LNC(6) FH_LNC(8) FH_LNC(12) FH_LNC(16)
+    default: return hipErrorInvalidValue;
+    }
+#undef FH_LNC
     return hipGetLastError();
 }
 hipError_t pool(const float *x32, const int32_t *offsets, int nseq, int max_len, int H, int cls_compact, int mean,

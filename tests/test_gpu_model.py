@@ -211,13 +211,15 @@ def test_rope_before_attention_equals_rope_inside(monkeypatch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,lens", [("minilm-l6", (100, 7, 64, 65, 128, 1)), ("nomic-bert", (700, 20, 257, 129))])
+@pytest.mark.parametrize("name,lens", [("minilm-l6", (100, 7, 64, 65, 128, 1)), ("nomic-bert", (700, 20, 257, 129)),
+                                       ("bge-small", (100, 7, 128, 1)), ("bge-small-q8", (60, 9, 33))])
 def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
-    """Mean pooling applies the last LayerNorm inside its segment sums
-    (fh::ln_pool); with FUTON_LN_POOL=0 the LayerNorm writes the float32
-    rows and the pooling reads them back.  Same normalized values, summed in
-    another order (eight-row groups inside each 64-token segment), so the
-    vectors agree to float32 rounding, and batch ≡ single still holds."""
+    """Pooling applies the last LayerNorm itself; with FUTON_LN_POOL=0 the
+    LayerNorm writes the float32 rows and the pooling reads them back.  Mean
+    pooling (fh::ln_pool) adds the same normalized values in another order
+    (eight-row groups inside each 64-token segment), so the vectors agree to
+    float32 rounding; CLS pooling (fh::ln_cls_pool, binary16 rows or the Q8
+    path's float32 rows) gives the same bits.  Batch ≡ single holds."""
     w = synth.workload(name)
     tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
     parts = [synth.make_batch(w.ids_seed + 21 + i, 1, L, L)[0] for i, L in enumerate(lens)]
@@ -229,6 +231,8 @@ def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
     apart = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
     a = fused.EncodePacked(ids, offsets, w.out_dim)
     b = apart.EncodePacked(ids, offsets, w.out_dim)
+    if w.config["pooling"] == "cls":
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.abs(a - b).max()
     assert np.abs(a - b).max() < 2e-6, np.abs(a - b).max()
     cos = np.sum(a * b, axis=1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
     assert cos.min() > 0.9999999, cos.min()
