@@ -840,8 +840,10 @@ int mlp_fused(fh_model *m, const DevLayer &L, const f16 *attn, const f16 *ya, co
 // C = f16(A·Wᵀ + bias + (yr − mean)·rstd·γ + β), yr's statistics from
 // row_stats.
 int gemm_resln(fh_model *m, int cls, const DevMat &w, const void *A, int M, const float *bias, const f16 *yr,
-               const f32x2 *stats, const float *gamma, const float *beta, f16 *C, hipStream_t s) {
+               const f32x2 *stats, const float *gamma, const float *beta, f16 *C, hipStream_t s,
+               const int32_t *res_map = nullptr) {
     GemmArgs g{};
+    g.res_map = res_map;
     g.A = A;
     g.B = w.w;
     g.bias = bias;
@@ -966,7 +968,14 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int M = last_cls ? S : T;
         f16 *yA = last_cls ? m->xc16 : m->x16, *yBo = last_cls ? m->yBc : yB;
         f32x2 *sA = last_cls ? m->sAc : m->sA, *sB = last_cls ? m->sBc : m->sB;
-        if (last_cls) {
+        const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
+        if (next && !next->qkv.wm) next = nullptr;
+        const bool fused = use_mlp(L, M, I, next != nullptr);
+        // The CLS rows' residual: gathered into compact rows, except where
+        // the output projection runs on the tiled GEMM, which reads the CLS
+        // rows of the full-token stream through a row map (the offsets).
+        const bool res_map = last_cls && !fused && !fh::gemm_ring_worth(M, L.out.n);
+        if (last_cls && !res_map) {
             Scope sc(m, K_CLS_TAIL, 0.0, (double)S * (H * 4 + 16), s);
             LCHK(fh::gather_rows(nullptr, m->x16, m->sA, b.d_offsets, S, H, nullptr, m->xc16, m->sAc, s));
         }
@@ -975,9 +984,7 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
         const int kOut = K_GEMM_OUT, kFfn1 = K_GEMM_FFN1, kFc2 = K_GEMM_FC2;
 
         sa_ready = qkv_ready = false;
-        const DevLayer *next = last ? nullptr : &m->layers[(size_t)li + 1];
-        if (next && !next->qkv.wm) next = nullptr;
-        if (use_mlp(L, M, I, next != nullptr)) {
+        if (fused) {
             // yB = attn·Woᵀ + b + LN(yA), then the feed-forward block, in one
             // kernel: yB stays on-chip, its statistics are computed there,
             // and (unless this is the last layer) so are the new yA's for the
@@ -994,7 +1001,8 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
             continue;
         }
         // yB = attn·Woᵀ + b + LN(yA)  (model.go:596-599)
-        if ((rc = gemm_resln(m, kOut, L.out, last_cls ? m->attnc : m->attn, M, L.out_b, yA, sA, gA, bA, yBo, s)))
+        if ((rc = gemm_resln(m, kOut, L.out, last_cls ? m->attnc : m->attn, M, L.out_b, res_map ? m->x16 : yA,
+                             res_map ? m->sA : sA, gA, bA, yBo, s, res_map ? b.d_offsets : nullptr)))
             return rc;
         if ((rc = checkpoint(m, b, cp, s))) return rc;
 

@@ -44,6 +44,10 @@ struct GemmArgs {
     const float *c2;     // LN_IN: [N] Σ_k W[n,k]·β[k] + bias[n]
     const f32x2 *stats_in;      // [M] (mean, rstd) of A's rows (LN_IN) or of resid_h's rows (RES_LN)
     const float *ln_g, *ln_b;   // RES_LN: γ, β of resid_h's LayerNorm
+    // Tiled kernel only: output row r takes its residual (and, with RES_LN,
+    // its statistics) from row res_map[r] of resid/resid_h (stats_in), or
+    // from row r when null.
+    const int32_t *res_map;
 };
 
 // Fused feed-forward block (mlp.hip), hidden width 384:

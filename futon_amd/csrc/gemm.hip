@@ -98,10 +98,11 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs &g, int row, int c
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
     }
+    const size_t rrow = g.res_map ? (size_t)g.res_map[row] : (size_t)row;
     if (g.resid) {
-        v += *(const f32x4 *)(g.resid + (size_t)row * g.ldr + col);
+        v += *(const f32x4 *)(g.resid + rrow * g.ldr + col);
     } else if (g.resid_h) {
-        const f16x4 r = *(const f16x4 *)(g.resid_h + (size_t)row * g.ldr + col);
+        const f16x4 r = *(const f16x4 *)(g.resid_h + rrow * g.ldr + col);
         if (LNM == fh::RES_LN) v += ln_resid(g, rs, col, r);
         else v += (f32x4){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
     }
@@ -123,7 +124,9 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &g, int m0, int n0, i
         const int rl = (wm * C::MT + tm) * 16 + (lane & 15);
         const int row = m0 + rl;
         if (row >= g.M) continue;
-        const f32x2 rs = LNM != fh::LN_NONE ? g.stats_in[row] : (f32x2){0.f, 0.f};
+        const f32x2 rs = LNM == fh::RES_LN  ? g.stats_in[g.res_map ? g.res_map[row] : row]
+                         : LNM == fh::LN_IN ? g.stats_in[row]
+                                            : (f32x2){0.f, 0.f};
         float sa = 0.f;
         if (I8) sa = g.a_scale[row];
 #pragma unroll
@@ -242,10 +245,11 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
                 const int gcol = ocol0 + ch * 8;
                 f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = r0;
                 if (g.resid_h) {
-                    const f16x8 rr = *(const f16x8 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                    const int rgrow = g.res_map ? g.res_map[grow] : grow;
+                    const f16x8 rr = *(const f16x8 *)(g.resid_h + (size_t)rgrow * g.ldr + gcol);
                     const f16x4 ra = {rr[0], rr[1], rr[2], rr[3]}, rb = {rr[4], rr[5], rr[6], rr[7]};
                     if (LNM == fh::RES_LN) {
-                        const f32x2 st = g.stats_in[grow];
+                        const f32x2 st = g.stats_in[rgrow];
                         r0 = ln_resid(g, st, gcol, ra);
                         r1 = ln_resid(g, st, gcol + 4, rb);
                     } else {
@@ -277,10 +281,11 @@ __device__ __forceinline__ void store_tiles_lds(const GemmArgs &g, int m0, int n
             const int gcol = ocol0 + ch * (16 / ESZ);
             if (OUT_F32 && (g.resid || g.resid_h)) {
                 f32x4 v = __builtin_bit_cast(f32x4, d);
+                const size_t rgrow = g.res_map ? (size_t)g.res_map[grow] : (size_t)grow;
                 if (g.resid) {
-                    v += *(const f32x4 *)(g.resid + (size_t)grow * g.ldr + gcol);
+                    v += *(const f32x4 *)(g.resid + rgrow * g.ldr + gcol);
                 } else {
-                    const f16x4 rr = *(const f16x4 *)(g.resid_h + (size_t)grow * g.ldr + gcol);
+                    const f16x4 rr = *(const f16x4 *)(g.resid_h + rgrow * g.ldr + gcol);
                     v += (f32x4){(float)rr[0], (float)rr[1], (float)rr[2], (float)rr[3]};
                 }
                 d = __builtin_bit_cast(i32x4, v);

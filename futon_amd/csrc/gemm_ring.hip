@@ -569,7 +569,7 @@ bool gemm_ring_worth(int M, int N) {
 }
 
 bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
-    if (g.M <= 0 || g.N % BN != 0 || g.K % 64 != 0 || g.K <= 0) return false;
+    if (g.M <= 0 || g.N % BN != 0 || g.K % 64 != 0 || g.K <= 0 || g.res_map) return false;
     if (act != ACT_NONE && act != ACT_GELU && act != ACT_RES16 && act != ACT_SWIGLU) return false;
     // SwiGLU: binary16 out, ldc ≥ N/2, no residual
     if (act == ACT_SWIGLU && (out_f32 || g.resid || g.resid_h || ln == RES_LN || g.ldc < g.N / 2)) return false;
@@ -585,6 +585,7 @@ bool gemm_ring_ok(const GemmArgs &g, int act, bool out_f32, int ln) {
 }
 
 bool gemm_ring_q8_ok(const GemmArgs &g, int act, bool out_f32) {
+    if (g.res_map) return false;
     if (g.M <= 0 || g.N % BN != 0 || g.K % 128 != 0 || g.K <= 0) return false;
     if (act != ACT_NONE && act != ACT_GELU) return false;
     if (!g.a_scale || !g.b_scale || g.resid_h || (g.resid && !out_f32)) return false;
