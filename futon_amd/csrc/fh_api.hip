@@ -204,6 +204,10 @@ struct fh_model {
     // FUTON_LN_POOL=0 keeps the LayerNorm and the pooling apart (diagnostics;
     // for mean pooling the segment sums are then added in another order).
     bool ln_pool = false;
+    // The embedding kernel also writes the first layer's row statistics
+    // (binary16 folded path; FUTON_EMBED_STATS=0 leaves them to row_stats:
+    // diagnostics, the same bits).
+    bool embed_stats = false;
     hipStream_t stream = nullptr;
     float *word = nullptr, *pos = nullptr, *type0 = nullptr, *emb_w = nullptr, *emb_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -922,10 +926,15 @@ int run_forward_fold(fh_model *m, const BatchInfo &b, hipStream_t s) {
     int cp = 0, rc;
     {
         Scope sc(m, K_EMBED, 0.0, (double)T * H * (4 + (m->pos ? 4 : 0) + 2) + T * 4.0, s);
-        LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, nullptr, nullptr, 0.f, H,
-                          nullptr, m->x16, s));
+        // The first layer's QKV fold needs the sum's row statistics: written
+        // here with it where the kernel covers the width.
+        LCHK(fh::embed_ln(b.d_ids, b.d_offsets, S, b.max_len, m->word, m->type0, m->pos, nullptr, nullptr,
+                          (float)c.layer_norm_eps, H, nullptr, m->x16, s, nullptr, nullptr, 0,
+                          m->embed_stats ? m->sA : nullptr));
     }
-    bool sa_ready = false;   // sA already holds yA's statistics (written by the previous fused kernel)
+    // sA already holds yA's statistics (written by the embedding kernel or
+    // the previous fused kernel)
+    bool sa_ready = m->embed_stats;
     bool qkv_ready = false;  // qkv already holds this layer's projection (ditto)
     for (int li = 0; li < c.num_layers; li++) {
         const DevLayer &L = m->layers[(size_t)li];
@@ -1375,6 +1384,8 @@ extern "C" int fh_model_create(const fh_config *cfg, const fh_tensor *tensors, i
     {
         const char *lp = getenv("FUTON_LN_POOL");
         m->ln_pool = !(lp && lp[0] == '0') && fh::ln_pool_ok(H);
+        const char *es = getenv("FUTON_EMBED_STATS");
+        m->embed_stats = !(es && es[0] == '0') && fh::embed_stats_ok(H);
     }
     *out = m;
     return FH_OK;

@@ -201,7 +201,10 @@ hipError_t rope_qk(f16 *qkv, const int32_t *offsets, int nseq, int max_len, int 
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s, int8_t *q = nullptr,
-                    float *qs = nullptr, int T = 0);
+                    float *qs = nullptr, int T = 0, f32x2 *st = nullptr);
+// Whether embed_ln can also write the un-normalized rows' (mean, rstd) (st,
+// gamma null: row_stats' values, eps the LayerNorm's).
+bool embed_stats_ok(int H);
 // y32 or y16 (exactly one non-null) holds proj + bias + residual; q
 // non-null (with x32): also the normalized rows' int8 codes and scales.
 hipError_t layer_norm(const float *y32, const f16 *y16, int M, int H, const float *gamma, const float *beta,

@@ -319,39 +319,64 @@ __global__ __launch_bounds__(256) void layer_norm_v_kernel(const T *y, int M, co
         if (q) quant_row_v<VPL>(v1, lane, q + (size_t)(row + 1) * H, qs + row + 1);
     }
 }
+// With gamma null: the un-normalized sum in binary16 for a consumer that
+// folds this LayerNorm, and, when st is set, its rows' (mean, rstd) as
+// row_stats_kernel computes them from those binary16 values: the block's four
+// rows are staged in LDS and wave 0 reduces them with row_stats' lane layout
+// (16 lanes a row), so the statistics are the same bits without a second
+// pass over the rows.  (Each wave reducing its own row, every 16-lane group
+// the same one, measured slower: four times the float64 work a block.)
 template <int VPL>
 __global__ __launch_bounds__(256) void embed_ln_v_kernel(const int32_t *ids, const int32_t *offsets,
                                                          const float *word, const float *type0, const float *pos,
                                                          const float *gamma, const float *beta, float eps,
-                                                         float *x32, f16 *x16, int8_t *q, float *qs) {
+                                                         float *x32, f16 *x16, int8_t *q, float *qs, f32x2 *st) {
     constexpr int H = 64 * VPL;
+    __shared__ __attribute__((aligned(16))) f16 srow[4][H];
     const int seq = blockIdx.y;
     const int start = offsets[seq], L = offsets[seq + 1] - start;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= L) return;
+    const bool stats = H % 128 == 0 && !gamma && st;  // block-uniform: every wave reaches the barrier below
+    if (t >= L && !stats) return;
     const int lane = threadIdx.x & 63;
     const size_t row = (size_t)(start + t);
-    float v[VPL], u[VPL];
-    ld_row<VPL>(word + (size_t)ids[row] * H, lane, v);
-    if (type0) {
-        ld_row<VPL>(type0, lane, u);
+    if (t < L) {
+        float v[VPL], u[VPL];
+        ld_row<VPL>(word + (size_t)ids[row] * H, lane, v);
+        if (type0) {
+            ld_row<VPL>(type0, lane, u);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) v[j] += u[j];
-    }
-    if (pos) {
-        ld_row<VPL>(pos + (size_t)t * H, lane, u);
+            for (int j = 0; j < VPL; ++j) v[j] += u[j];
+        }
+        if (pos) {
+            ld_row<VPL>(pos + (size_t)t * H, lane, u);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) v[j] += u[j];
+            for (int j = 0; j < VPL; ++j) v[j] += u[j];
+        }
+        if (!gamma) {  // un-normalized sum, for a consumer that folds this LayerNorm
+            st_row<VPL>(nullptr, x16 + row * H, lane, v);
+            if (stats) st_row<VPL>(nullptr, srow[threadIdx.x >> 6], lane, v);
+        } else {
+            float gw[VPL], gb[VPL];
+            ld_row<VPL>(gamma, lane, gw);
+            ld_row<VPL>(beta, lane, gb);
+            ln_row_v<VPL>(v, gw, gb, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
+            if (q) quant_row_v<VPL>(v, lane, q + row * H, qs + row);
+        }
     }
-    if (!gamma) {  // un-normalized sum, for a consumer that folds this LayerNorm
-        st_row<VPL>(nullptr, x16 + row * H, lane, v);
-        return;
+    if constexpr (H % 128 == 0) {
+        if (!stats) return;
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            constexpr int C = H / 128;
+            const int r = lane >> 4, l16 = lane & 15, tr = blockIdx.x * 4 + r;
+            f16x8 w8[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) w8[c] = *(const f16x8 *)&srow[r][(c * 16 + l16) * 8];
+            const f32x2 rs = fh_rs::row_stats16<C>(w8, eps);
+            if (l16 == 0 && tr < L) st[start + tr] = rs;
+        }
     }
-    float gw[VPL], gb[VPL];
-    ld_row<VPL>(gamma, lane, gw);
-    ld_row<VPL>(beta, lane, gb);
-    ln_row_v<VPL>(v, gw, gb, eps, x32 ? x32 + row * H : nullptr, x16 + row * H);
-    if (q) quant_row_v<VPL>(v, lane, q + row * H, qs + row);
 }
 
 __device__ double block_sum_f64(double v, double *red) {
@@ -550,15 +575,17 @@ __global__ __launch_bounds__(256) void ln_cls_pool_kernel(const T *__restrict__ 
 }  // namespace
 
 namespace fh {
+bool embed_stats_ok(int H) { return H % 128 == 0 && (H / 64 == 4 || H / 64 == 6 || H / 64 == 8 || H / 64 == 12 || H / 64 == 16); }
 hipError_t embed_ln(const int32_t *ids, const int32_t *offsets, int nseq, int max_len,
                     const float *word, const float *type0, const float *pos, const float *gamma,
                     const float *beta, float eps, int H, float *x32, f16 *x16, hipStream_t s, int8_t *q,
-                    float *qs, int T) {
+                    float *qs, int T, f32x2 *st) {
     if (nseq <= 0) return hipSuccess;
+    if (st && (gamma || !embed_stats_ok(H))) return hipErrorInvalidValue;
     const dim3 grid((max_len + 3) / 4, nseq);
 #define FH_EMB_V(V)                                                                                          \
     case V: hipLaunchKernelGGL(embed_ln_v_kernel<V>, grid, dim3(256), 0, s, ids, offsets, word, type0, pos, gamma, \
-                               beta, eps, x32, x16, gamma ? q : nullptr, qs);                                \
+                               beta, eps, x32, x16, gamma ? q : nullptr, qs, st);                            \
         return hipGetLastError();
     if (H % 64 == 0) {
         switch (H / 64) {

@@ -243,6 +243,27 @@ def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name,batch", [("minilm-l6", 24), ("bge-small", 300), ("bert-base", 3)])
+def test_embedding_statistics_equal_row_stats(name, batch, monkeypatch):
+    """The embedding kernel writes the first layer's row statistics itself,
+    in row_stats' reduction order over the same binary16 values; the forward
+    returns the same bits as with the separate row_stats launch
+    (FUTON_EMBED_STATS=0)."""
+    w = synth.workload(name)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    ids, offsets = synth.make_batch(w.ids_seed + 31, batch, w.len_lo, w.len_hi)
+    native = _native()
+    fused = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    monkeypatch.setenv("FUTON_EMBED_STATS", "0")
+    apart = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    a = fused.EncodePacked(ids, offsets, w.out_dim)
+    b = apart.EncodePacked(ids, offsets, w.out_dim)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.abs(a - b).max()
+    fused.close()
+    apart.close()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name,batch", [("minilm-l6", 192), ("bge-small", 192)])
 def test_fused_mlp_forward_equals_two_gemms(name, batch, monkeypatch):
     """At hidden width 384 the feed-forward block runs as one fused kernel
