@@ -211,24 +211,28 @@ def test_rope_before_attention_equals_rope_inside(monkeypatch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name,lens", [("minilm-l6", (100, 7, 64, 65, 128, 1)), ("nomic-bert", (700, 20, 257, 129)),
-                                       ("bge-small", (100, 7, 128, 1)), ("bge-small-q8", (60, 9, 33))])
-def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
+@pytest.mark.parametrize("name,lens,q8", [("minilm-l6", (100, 7, 64, 65, 128, 1), False),
+                                          ("nomic-bert", (700, 20, 257, 129), False),
+                                          ("bge-small", (100, 7, 128, 1), False), ("bge-small-q8", (60, 9, 33), True),
+                                          ("minilm-l6", (90, 5, 129), True)])
+def test_ln_pool_matches_separate_layer_norm(name, lens, q8, monkeypatch):
     """Pooling applies the last LayerNorm itself; with FUTON_LN_POOL=0 the
     LayerNorm writes the float32 rows and the pooling reads them back.  Mean
     pooling (fh::ln_pool) adds the same normalized values in another order
     (eight-row groups inside each 64-token segment), so the vectors agree to
     float32 rounding; CLS pooling (fh::ln_cls_pool, binary16 rows or the Q8
-    path's float32 rows) gives the same bits.  Batch ≡ single holds."""
+    path's float32 rows) gives the same bits.  Batch ≡ single holds.  The
+    Q8 path (float32 residual stream) runs both kinds: MiniLM-L6 with Q8
+    weights pools by mean from float32 rows."""
     w = synth.workload(name)
-    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=w.q8)
+    tensors = synth.make_tensors(w.config, w.weight_seed, biases=w.extra.get("biases", True), q8=q8)
     parts = [synth.make_batch(w.ids_seed + 21 + i, 1, L, L)[0] for i, L in enumerate(lens)]
     ids = np.concatenate(parts).astype(np.int32)
     offsets = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
     native = _native()
-    fused = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    fused = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=q8)
     monkeypatch.setenv("FUTON_LN_POOL", "0")
-    apart = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=w.q8)
+    apart = native.Model(native.PackConfig.from_dict(w.config), tensors, q8=q8)
     a = fused.EncodePacked(ids, offsets, w.out_dim)
     b = apart.EncodePacked(ids, offsets, w.out_dim)
     if w.config["pooling"] == "cls":
@@ -238,6 +242,9 @@ def test_ln_pool_matches_separate_layer_norm(name, lens, monkeypatch):
     assert cos.min() > 0.9999999, cos.min()
     single = fused.EncodePacked(parts[1], np.array([0, len(parts[1])], dtype=np.int32), w.out_dim)
     assert np.array_equal(single[0].view(np.uint32), a[1].view(np.uint32))
+    want = oracle.Model(w.config, tensors, q8=q8).encode_batch(ids, offsets, w.out_dim, threads=16)
+    ocos = [packio.cosine(a[i], want[i]) for i in range(len(lens))]
+    assert min(ocos) >= COS_GATE, (name, q8, min(ocos))
     fused.close()
     apart.close()
 
